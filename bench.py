@@ -1,0 +1,215 @@
+"""Benchmark of the MI355X VSA hot path (one JSON line on stdout).
+
+Workload (the metric's configuration): fused VSA
+forward + backward, B=1, H=40, S=40,960, D=128, bf16, block (4,8,8) -> 256
+tokens, 160 full blocks, topk=20, gate ~ U(0,1) of shape [B,H,S,D];
+q, k, v, dO ~ N(0,1).  A step is one forward + backward of ``vsa.mi355x_vsa``
+over that synthetic batch, inputs resident in HBM.
+
+value = effective TFLOP/s = 3.5 * 4*B*H*Qb*topk*be^2*D / step time (only the
+selected block pairs count; recompute does not).  Beside it: per-kernel HIP
+event timings (the roofline of the dominant kernel) and the CPU oracle timed
+on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "simple-vsa_amd"))
+
+MFMA_BF16_PEAK_TFLOPS = 2516.6   # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0
+
+CFG = dict(B=1, H=40, S=40960, D=128, block=(4, 8, 8), topk=20)
+
+
+def flops_fwd(B, H, S, D, be, topk):
+    return 4.0 * B * H * (S // be) * topk * be * be * D
+
+
+def _events_time(fn, iters):
+    import torch
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def cpu_baseline(heads: int = 1):
+    """The CPU oracle (a restatement of torch_vsa) fwd+bwd on `heads` heads of
+    the workload; returns (TFLOP/s, seconds, threads)."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import vsa_oracle as O
+    threads = torch.get_num_threads()
+    B, S, D, topk = CFG["B"], CFG["S"], CFG["D"], CFG["topk"]
+    be = math.prod(CFG["block"])
+    g = torch.Generator().manual_seed(0)
+    shape = (B, heads, S, D)
+    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16).requires_grad_()
+                   for _ in range(4))
+    gate = torch.rand(shape, generator=g).to(torch.bfloat16).requires_grad_()
+    vbs = torch.full((S // be,), be)
+    t0 = time.perf_counter()
+    out = O.torch_vsa(q, k, v, vbs, vbs, topk, CFG["block"], gate)
+    torch.autograd.grad(out, (q, k, v, gate), do.detach())
+    dt = time.perf_counter() - t0
+    f = 3.5 * flops_fwd(B, heads, S, D, be, topk)
+    return f / dt / 1e12, dt, threads
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--kernels-only", action="store_true", help="skip the CPU baseline and summary")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every MI355X box "
+              "in this setup has a single GPU.  Per-GPU sharding is by heads; see DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vsa import mi355x as M
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, H, S, D, topk = CFG["B"], CFG["H"], CFG["S"], CFG["D"], CFG["topk"]
+    be = math.prod(CFG["block"])
+    nb = S // be
+    scale = 1.0 / math.sqrt(D)
+    g = torch.Generator(device=dev).manual_seed(0)
+    shape = (B, H, S, D)
+    q, k, v, do = (torch.randn(shape, generator=g, device=dev, dtype=torch.bfloat16)
+                   for _ in range(4))
+    gate = torch.rand(shape, generator=g, device=dev, dtype=torch.bfloat16)
+    vbs = torch.full((nb,), be, device=dev, dtype=torch.int32)
+    for t in (q, k, v, gate):
+        t.requires_grad_()
+
+    def step():
+        out = M.mi355x_vsa(q, k, v, vbs, vbs, topk, CFG["block"], gate)
+        torch.autograd.grad(out, (q, k, v, gate), do)
+
+    def fwd_only():
+        with torch.no_grad():
+            M.mi355x_vsa(q, k, v, vbs, vbs, topk, CFG["block"], gate)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    fwd_ms = _events_time(fwd_only, max(5, args.steps // 2))
+
+    # ---- per-kernel timings (HIP events on the launch stream) -------------
+    F_fwd = flops_fwd(B, H, S, D, be, topk)
+    with torch.no_grad():
+        qd, kd, vd, gd = (t.detach() for t in (q, k, v, gate))
+        qc, kc, vc = M.block_mean_qkv(qd, kd, vd, vbs, vbs, be)
+        _, probs, outc, sel = M.coarse_forward(qc, kc, vc, topk, scale)
+        out, lse = M.sparse_forward(qd, kd, vd, sel, vbs, be, scale, out_c=outc, gate=gd)
+        delta, d_outc, _ = M.backward_prep(out, do, be, out_c=outc, gate=gd)
+        dqc, dkc, dvc = M.coarse_backward(qc, kc, vc, probs, d_outc, scale)
+        inverse, offsets, counts = M.invert_routes(sel, nb)
+        from vsa import _lib
+        code, st = _lib.dtype_code(qd.dtype), _lib.stream_of(qd)
+        dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+
+        def k_dq():
+            _lib.call("vsa_sparse_bwd_dq", _lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd), _lib.ptr(do),
+                      _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(sel), _lib.ptr(vbs), _lib.ptr(dq),
+                      _lib.ptr(dqc), _lib.ptr(vbs), B * H, S, S, D, be, topk, scale, code, st)
+
+        def k_dkdv():
+            _lib.call("vsa_sparse_bwd_dkdv", _lib.ptr(qd), _lib.ptr(kd), _lib.ptr(vd),
+                      _lib.ptr(do), _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(counts),
+                      _lib.ptr(offsets), _lib.ptr(inverse), _lib.ptr(vbs), _lib.ptr(dk),
+                      _lib.ptr(dv), _lib.ptr(dkc), _lib.ptr(dvc), B * H, S, S, D, be, topk,
+                      scale, code, st)
+
+        it = 10
+        kt = {
+            "pool_qkv": (_events_time(lambda: M.block_mean_qkv(qd, kd, vd, vbs, vbs, be), it),
+                         None),
+            "coarse_fwd_topk": (_events_time(lambda: M.coarse_forward(qc, kc, vc, topk, scale), it),
+                                None),
+            "sparse_fwd": (_events_time(lambda: M.sparse_forward(qd, kd, vd, sel, vbs, be, scale,
+                                                                 out_c=outc, gate=gd), it),
+                           F_fwd),
+            "bwd_prep": (_events_time(lambda: M.backward_prep(out, do, be, out_c=outc, gate=gd),
+                                      it), None),
+            "coarse_bwd": (_events_time(lambda: M.coarse_backward(qc, kc, vc, probs, d_outc,
+                                                                  scale), it), None),
+            "csr_build": (_events_time(lambda: M.invert_routes(sel, nb), it), None),
+            "sparse_bwd_dq": (_events_time(k_dq, it), 1.5 * F_fwd),
+            "sparse_bwd_dkdv": (_events_time(k_dkdv, it), 1.0 * F_fwd),
+        }
+    kernels = {n: {"ms": round(t, 4)} for n, (t, _) in kt.items()}
+    for n, (t, f) in kt.items():
+        if f:
+            kernels[n]["tflops_algorithmic"] = round(f / (t * 1e-3) / 1e12, 1)
+    dom = max((n for n in kt if kt[n][1]), key=lambda n: kt[n][0])
+    dom_t, dom_f = kt[dom]
+    achieved = dom_f / (dom_t * 1e-3) / 1e12
+
+    F_total = 3.5 * F_fwd
+    value = F_total / (ms_step * 1e-3) / 1e12
+    cpu = None
+    if not (args.no_cpu or args.kernels_only):
+        cv, cs, cth = cpu_baseline(heads=1)
+        cpu = {"value": round(cv, 4), "unit": "TFLOP/s", "cores": cth, "kind": "port",
+               "sample": f"oracle torch_vsa fwd+bwd, 1 of {H} heads of the workload "
+                         f"(B=1,H=1,S={S},D={D},be={be},topk={topk}, bf16 inputs), "
+                         f"{cs:.1f} s wall, throughput in effective TFLOP/s"}
+    line = {
+        "metric": "VSA fwd+bwd ms & effective TFLOP/s (% bf16 MFMA peak) at 40k tokens, block 256",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "fwd_ms": round(fwd_ms, 4),
+        "bwd_ms": round(ms_step - fwd_ms, 4),
+        "pct_bf16_peak": round(100 * value / MFMA_BF16_PEAK_TFLOPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (q,k,v,dO ~ N(0,1), gate ~ U(0,1), seed 0)",
+        "config": {"workload": "Video-DiT mid shape (BASELINE configs[2])", "B": B, "H": H,
+                   "seq_len": S, "head_dim": D, "block_size": list(CFG["block"]),
+                   "block_elements": be, "topk": topk, "gate": "[B,H,S,D]",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

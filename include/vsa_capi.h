@@ -1,0 +1,178 @@
+/*
+ * vsa_capi.h -- C ABI of the MI355X (gfx950) Video Sparse Attention kernels.
+ *
+ * This is the drop-in boundary under the reference's Python operator API
+ * (ita9naiwa/simple-vsa): the host layer binds these symbols with ctypes and
+ * keeps the reference's `*_vsa(q, k, v, variable_block_sizes,
+ * q_variable_block_sizes, topk, block_size, compress_attn_weight)` and
+ * `*_sparse_attention(q, k, v, selected, variable_block_sizes, *, block_size,
+ * sm_scale)` signatures above them.
+ *
+ * Rules shared by every entry point:
+ *  - plain device pointers, element counts and a hipStream_t passed as void*;
+ *    no framework types cross this boundary;
+ *  - tensors are contiguous row-major; q-like tensors are [BH, Sq, D], k/v-like
+ *    [BH, Skv, D], block vectors [BH, nblocks, D], where BH = batch * heads;
+ *  - dtype: VSA_BF16 or VSA_F16 for every kernel; VSA_F32 is accepted by the
+ *    bandwidth kernels (pooling, coarse, Top-K, CSR, combine/prep) only;
+ *  - nothing here allocates or frees device memory: every output and every
+ *    workspace buffer is owned by the caller;
+ *  - launches are asynchronous on `stream`; no host synchronisation;
+ *  - return 0 on success, a negative VSA_ERR_* code otherwise (no exceptions
+ *    cross the ABI); vsa_status_string() turns a code into text;
+ *  - route ids outside [0, Kb) contribute nothing; block sizes are clamped to
+ *    [0, block_elements] for token masking.
+ */
+#ifndef VSA_CAPI_H
+#define VSA_CAPI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum vsa_dtype { VSA_BF16 = 0, VSA_F16 = 1, VSA_F32 = 2 };
+
+/* How compress_attn_weight is laid out: absent, [BH, Sq, D], or [BH, Sq, 1]. */
+enum vsa_gate_mode { VSA_GATE_NONE = 0, VSA_GATE_FULL = 1, VSA_GATE_PER_TOKEN = 2 };
+
+enum vsa_status {
+  VSA_OK = 0,
+  VSA_ERR_NULL = -1,        /* a required pointer is NULL */
+  VSA_ERR_SHAPE = -2,       /* sizes inconsistent or out of range */
+  VSA_ERR_DTYPE = -3,       /* dtype not supported by this entry point */
+  VSA_ERR_UNSUPPORTED = -4, /* (block_elements, head_dim) pair has no kernel */
+  VSA_ERR_LAUNCH = -5       /* the HIP launch itself failed */
+};
+
+/* Text for a status code (static storage). */
+const char* vsa_status_string(int status);
+
+/* Library version string (static storage). */
+const char* vsa_version(void);
+
+/*
+ * Padded block mean of q, k and v in one launch.
+ * Replaces fused_block_mean x3 (fused_common.py:20-59, 106-144, 340-347;
+ * called from common.py:155-157).  out[bh, n, :] = T(sum_{t < vbs[n]}
+ * x[bh, n*be + t, :] / max(vbs[n], 1)), fp32 sum.
+ */
+int vsa_pool_qkv(const void* q, const void* k, const void* v,
+                 const int32_t* q_vbs, const int32_t* kv_vbs,
+                 void* q_c, void* k_c, void* v_c,
+                 int64_t bh, int64_t sq, int64_t skv, int32_t head_dim,
+                 int32_t block_elements, int32_t dtype, void* stream);
+
+/*
+ * Coarse block attention on the pooled tokens plus Top-K routing.
+ * Replaces coarse_branch_compact's matmul/softmax/matmul (common.py:159-166)
+ * and scores.topk (triton_impl.py:1710; torch_impl.py:85).
+ *   scores[bh, i, j] = T(T(q_c[i] . k_c[j]) * scale)      (stored as fp32)
+ *   probs[bh, i, j]  = T(softmax_j(scores[bh, i, :]))      (stored as fp32)
+ *   out_c[bh, i, :]  = T(sum_j probs[i, j] * v_c[j, :])
+ *   selected[bh, i, :] = the `topk` key blocks with the largest scores; ties go
+ *   to the smaller block id; written in ascending block-id order (int32).
+ * `selected` may be NULL (no routing).  Kb <= 8192.
+ */
+int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
+                   float* scores, float* probs, void* out_c, int32_t* selected,
+                   int64_t bh, int32_t q_blocks, int32_t kv_blocks, int32_t head_dim,
+                   int32_t topk, float scale, int32_t dtype, void* stream);
+
+/*
+ * Stand-alone Top-K over fp32 scores [rows, kv_blocks] -> int32 [rows, topk]
+ * with the same tie rule and output order as vsa_coarse_fwd.
+ * Replaces scores.topk(topk, dim=-1) (triton_impl.py:1710).
+ */
+int vsa_topk(const float* scores, int32_t* selected, int64_t rows,
+             int32_t kv_blocks, int32_t topk, void* stream);
+
+/*
+ * Compact KV-block -> query-block CSR per (batch, head).
+ * Replaces _invert_indices (triton_impl.py:544-595): counts [BH, Kb],
+ * offsets [BH, Kb] (exclusive prefix of counts), inverse [BH, Qb*topk].
+ * Unlike the reference's atomic cursor, every segment is written in ascending
+ * query-block order, so the result is deterministic.
+ */
+int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
+                  int32_t* inverse, int64_t bh, int32_t q_blocks, int32_t kv_blocks,
+                  int32_t topk, void* stream);
+
+/*
+ * Sparse fine forward over the selected KV blocks (bf16/fp16 MFMA, online
+ * softmax in base 2), optionally fused with the combine.
+ * Replaces _triton_sparse_attention_forward (triton_impl.py:358-473: T6/T7
+ * kernels 39-355) and, when out_c != NULL, _FusedCombine.forward
+ * (fused_common.py:175-199, 261-295):
+ *   out = T(out_c[block] * gate + attn)   (gate = 1 when gate_mode == NONE)
+ *   out = T(attn)                          when out_c == NULL
+ *   lse[bh, q] = log2(sum_j exp2(scale*log2(e) * q.k_j))   (may be NULL)
+ * block_elements in {64, 128, 256}; head_dim in {64, 128}.
+ */
+int vsa_sparse_fwd(const void* q, const void* k, const void* v,
+                   const int32_t* selected, const int32_t* kv_vbs,
+                   void* out, float* lse, const void* out_c, const void* gate,
+                   int32_t gate_mode, int64_t bh, int64_t sq, int64_t skv,
+                   int32_t head_dim, int32_t block_elements, int32_t topk,
+                   float scale, int32_t dtype, void* stream);
+
+/*
+ * Backward preprocessing over dout: the softmax delta plus the combine
+ * gradients.  Replaces _delta_kernel/_delta_256_kernel (triton_impl.py:598-700)
+ * and _FusedCombine.backward (fused_common.py:202-256, 298-337).
+ *   attn  = out - out_c[block] * gate    (attn = out when out_c == NULL)
+ *   delta[bh, q]   = sum_d attn * dout                               (fp32)
+ *   d_out_c[bh, n] = T(sum_{t < be} T(dout * gate))     (if out_c != NULL)
+ *   d_gate         = T(dout * out_c[block])  (per token: summed over d)
+ */
+int vsa_bwd_prep(const void* out, const void* dout, const void* out_c, const void* gate,
+                 int32_t gate_mode, float* delta, void* d_out_c, void* d_gate,
+                 int64_t bh, int64_t sq, int32_t head_dim, int32_t block_elements,
+                 int32_t dtype, void* stream);
+
+/*
+ * Backward of the coarse branch (autograd of common.py:164-166 in T):
+ *   dP = T(d_out_c v_c^T); d_v_c = T(P^T d_out_c);
+ *   dS = T(scale * T(P * (dP - rowsum(P * dP))));
+ *   d_q_c = T(dS k_c); d_k_c = T(dS^T q_c).
+ * `ds` is fp32 workspace [BH, Qb, Kb].
+ */
+int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c, const float* probs,
+                   const void* d_out_c, float* ds, void* d_q_c, void* d_k_c, void* d_v_c,
+                   int64_t bh, int32_t q_blocks, int32_t kv_blocks, int32_t head_dim,
+                   float scale, int32_t dtype, void* stream);
+
+/*
+ * Query-owned dQ over the selected KV blocks.  Replaces _vsa_dq_256_kernel /
+ * _vsa_dq_kernel (triton_impl.py:703-969).  When d_q_c != NULL the pooled
+ * gradient is folded in: dq[t] += T(d_q_c[block] / max(q_vbs[block], 1)) for
+ * t < q_vbs[block] (block_mean backward, fused_common.py:62-103).
+ */
+int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
+                      const float* lse, const float* delta, const int32_t* selected,
+                      const int32_t* kv_vbs, void* dq, const void* d_q_c,
+                      const int32_t* q_vbs, int64_t bh, int64_t sq, int64_t skv,
+                      int32_t head_dim, int32_t block_elements, int32_t topk,
+                      float scale, int32_t dtype, void* stream);
+
+/*
+ * KV-owned dK/dV driven by the CSR from vsa_csr_build.  Replaces
+ * _vsa_dkdv_256_kernel / _vsa_dkdv_kernel (triton_impl.py:972-1318).  When
+ * d_k_c / d_v_c != NULL the pooled gradients are folded in as in
+ * vsa_sparse_bwd_dq (using kv_vbs).
+ */
+int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
+                        const float* lse, const float* delta, const int32_t* counts,
+                        const int32_t* offsets, const int32_t* inverse,
+                        const int32_t* kv_vbs, void* dk, void* dv,
+                        const void* d_k_c, const void* d_v_c,
+                        int64_t bh, int64_t sq, int64_t skv, int32_t head_dim,
+                        int32_t block_elements, int32_t topk, float scale,
+                        int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VSA_CAPI_H */

@@ -1,0 +1,541 @@
+// Bandwidth- and latency-bound kernels of the VSA common path on gfx950:
+// padded block mean, coarse block attention + Top-K routing, CSR inverse
+// routing, backward preprocessing (delta + combine gradients) and the coarse
+// branch backward.  The MFMA fine kernels live in fine_fwd.hip / fine_bwd.hip.
+#include "vsa_device.h"
+#include "vsa_launch.h"
+
+namespace vsa {
+
+// ---------------------------------------------------------------------------
+// Padded block mean (fused_common.py:20-59): one workgroup per (tensor, bh,
+// block); 16-byte coalesced loads over the valid rows only; fp32 sums reduced
+// across row groups in LDS; result rounded to T.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void pool_qkv_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ q_vbs, const int32_t* __restrict__ kv_vbs,
+    T* __restrict__ qc, T* __restrict__ kc, T* __restrict__ vc,
+    int64_t bh, int qb, int kb, int D, int be) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float part[256 * VEC];
+  int64_t id = blockIdx.x;
+  const int64_t nq = bh * qb, nk = bh * kb;
+  const T* x;
+  const int32_t* vbs;
+  T* out;
+  int nb;
+  if (id < nq) {
+    x = q; vbs = q_vbs; out = qc; nb = qb;
+  } else if (id < nq + nk) {
+    id -= nq; x = k; vbs = kv_vbs; out = kc; nb = kb;
+  } else {
+    id -= nq + nk; x = v; vbs = kv_vbs; out = vc; nb = kb;
+  }
+  const int n = (int)(id % nb);
+  const int32_t cnt = vbs[n];
+  const int valid = clamp_valid(cnt, be);
+  const float div = (float)(cnt > 1 ? cnt : 1);
+  const T* base = x + id * (int64_t)be * D;  // block id*: rows [n*be, n*be+be) of head id/nb
+  const int tpr = D / VEC, rpi = 256 / tpr;
+  const int col = threadIdx.x % tpr, row0 = threadIdx.x / tpr;
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  for (int t = row0; t < valid; t += rpi) {
+    u32x4 raw = *reinterpret_cast<const u32x4*>(base + (int64_t)t * D + col * VEC);
+    const T* vals = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] += Elem<T>::to_f(vals[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) part[row0 * D + col * VEC + e] = acc[e];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float s = 0.f;
+    for (int r = 0; r < rpi; ++r) s += part[r * D + d];
+    out[id * D + d] = Elem<T>::from_f(s / div);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Top-K by rank: element j is selected iff fewer than `topk` elements beat it,
+// where i beats j when s_i > s_j, or s_i == s_j and i < j.  Scores are compared
+// through a total-order integer key (-0 == +0; NaN above +inf, as torch.topk
+// ranks it), so the ranks are a permutation and exactly `topk` ids are chosen.
+// Selected ids are written in ascending id order.  `row` lives in LDS; `scan`
+// holds 256 ints.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int order_key(float x) {
+  uint32_t u = __float_as_uint(x + 0.0f);  // folds -0 into +0
+  if (x != x) u = 0x7fffffffu;             // NaN: larger than +inf
+  return (int)u >= 0 ? (int)u : (int)(u ^ 0x7fffffffu);
+}
+
+__device__ void topk_row(const float* row, int kb, int topk, int32_t* __restrict__ dst,
+                         int* scan) {
+  const int per = (kb + 255) / 256;
+  const int j0 = threadIdx.x * per;
+  unsigned flags = 0;  // bit m set: element j0+m selected (per <= 32)
+  int nsel = 0;
+  for (int m = 0; m < per; ++m) {
+    const int j = j0 + m;
+    if (j >= kb) break;
+    const int sj = order_key(row[j]);
+    int rank = 0;
+    for (int i = 0; i < kb; ++i) {
+      const int si = order_key(row[i]);
+      rank += (si > sj) || (si == sj && i < j);
+    }
+    if (rank < topk) {
+      flags |= 1u << m;
+      ++nsel;
+    }
+  }
+  // exclusive scan of nsel over the block (Hillis-Steele in LDS)
+  scan[threadIdx.x] = nsel;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    int add = threadIdx.x >= o ? scan[threadIdx.x - o] : 0;
+    __syncthreads();
+    scan[threadIdx.x] += add;
+    __syncthreads();
+  }
+  int pos = scan[threadIdx.x] - nsel;
+  for (int m = 0; m < per; ++m)
+    if ((flags & (1u << m)) && pos < topk) dst[pos++] = j0 + m;
+}
+
+constexpr int kMaxCoarseBlocks = 4096;  // keeps dynamic LDS under 64 KiB
+
+// One workgroup per (bh, query block): scores in T, softmax in T, out_c in T,
+// then Top-K on the scores row (common.py:159-166, triton_impl.py:1710).
+template <typename T>
+__global__ __launch_bounds__(256) void coarse_fwd_kernel(
+    const T* __restrict__ qc, const T* __restrict__ kc, const T* __restrict__ vc,
+    float* __restrict__ scores, float* __restrict__ probs, T* __restrict__ outc,
+    int32_t* __restrict__ selected, int qb, int kb, int D, int topk, float scale) {
+  extern __shared__ float smem[];
+  float* qrow = smem;            // D
+  float* srow = qrow + D;        // kb
+  float* prow = srow + kb;       // kb
+  float* red = prow + kb;        // 4
+  int* scan = reinterpret_cast<int*>(red + 4);  // 256
+  const int64_t b = blockIdx.y;
+  const int i = blockIdx.x;
+  const T* qsrc = qc + (b * qb + i) * D;
+  for (int d = threadIdx.x; d < D; d += 256) qrow[d] = Elem<T>::to_f(qsrc[d]);
+  __syncthreads();
+  const T* kbase = kc + b * kb * (int64_t)D;
+  float lmax = -INFINITY;
+  for (int j = threadIdx.x; j < kb; j += 256) {
+    const T* kr = kbase + (int64_t)j * D;
+    float dot = 0.f;
+    for (int d = 0; d < D; ++d) dot = fmaf(qrow[d], Elem<T>::to_f(kr[d]), dot);
+    const float s = round_t<T>(round_t<T>(dot) * scale);
+    srow[j] = s;
+    lmax = fmaxf(lmax, s);
+  }
+  const float mx = block_reduce<true>(lmax, red);
+  float lsum = 0.f;
+  for (int j = threadIdx.x; j < kb; j += 256) {
+    const float e = expf(srow[j] - mx);
+    prow[j] = e;
+    lsum += e;
+  }
+  const float sum = block_reduce<false>(lsum, red);
+  const int64_t rowoff = (b * qb + i) * (int64_t)kb;
+  for (int j = threadIdx.x; j < kb; j += 256) {
+    const float p = round_t<T>(prow[j] / sum);
+    prow[j] = p;
+    scores[rowoff + j] = srow[j];
+    probs[rowoff + j] = p;
+  }
+  __syncthreads();
+  const T* vbase = vc + b * kb * (int64_t)D;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < kb; ++j) acc = fmaf(prow[j], Elem<T>::to_f(vbase[(int64_t)j * D + d]), acc);
+    outc[(b * qb + i) * D + d] = Elem<T>::from_f(acc);
+  }
+  if (selected != nullptr) topk_row(srow, kb, topk, selected + (b * qb + i) * (int64_t)topk, scan);
+}
+
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ scores,
+                                                    int32_t* __restrict__ selected, int kb,
+                                                    int topk) {
+  extern __shared__ float smem[];
+  float* row = smem;
+  int* scan = reinterpret_cast<int*>(row + kb);
+  const int64_t r = blockIdx.x;
+  for (int j = threadIdx.x; j < kb; j += 256) row[j] = scores[r * kb + j];
+  __syncthreads();
+  topk_row(row, kb, topk, selected + r * topk, scan);
+}
+
+// ---------------------------------------------------------------------------
+// CSR inverse routing (triton_impl.py:476-595).
+// Pass 1 (one workgroup per bh): LDS histogram of the route, exclusive scan,
+// counts/offsets out, then an atomic-cursor scatter of query-block ids.
+// Pass 2 (one workgroup per (bh, kv)): put each segment in ascending order by a
+// histogram over query-block ids, which makes the layout deterministic.
+// ---------------------------------------------------------------------------
+__device__ void block_exclusive_scan(int* a, int n, int* tmp256) {
+  // sequential per-thread chunk sums + Hillis-Steele over 256 partials
+  const int per = (n + 255) / 256;
+  const int s0 = threadIdx.x * per;
+  int local = 0;
+  for (int m = 0; m < per && s0 + m < n; ++m) local += a[s0 + m];
+  tmp256[threadIdx.x] = local;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    int add = threadIdx.x >= o ? tmp256[threadIdx.x - o] : 0;
+    __syncthreads();
+    tmp256[threadIdx.x] += add;
+    __syncthreads();
+  }
+  int run = tmp256[threadIdx.x] - local;
+  for (int m = 0; m < per && s0 + m < n; ++m) {
+    const int c = a[s0 + m];
+    a[s0 + m] = run;
+    run += c;
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void csr_scatter_kernel(
+    const int32_t* __restrict__ selected, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ inverse, int qb, int kb, int topk) {
+  extern __shared__ int ismem[];
+  int* cnt = ismem;        // kb
+  int* cur = cnt + kb;     // kb
+  int* tmp = cur + kb;     // 256
+  const int64_t b = blockIdx.x;
+  const int edges = qb * topk;
+  const int32_t* sel = selected + b * edges;
+  for (int j = threadIdx.x; j < kb; j += 256) cnt[j] = 0;
+  __syncthreads();
+  for (int e = threadIdx.x; e < edges; e += 256) {
+    const int kv = sel[e];
+    if (kv >= 0 && kv < kb) atomicAdd(&cnt[kv], 1);
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < kb; j += 256) {
+    counts[b * kb + j] = cnt[j];
+    cur[j] = cnt[j];
+  }
+  __syncthreads();
+  block_exclusive_scan(cur, kb, tmp);
+  for (int j = threadIdx.x; j < kb; j += 256) offsets[b * kb + j] = cur[j];
+  __syncthreads();
+  int32_t* inv = inverse + b * edges;
+  for (int e = threadIdx.x; e < edges; e += 256) {
+    const int kv = sel[e];
+    if (kv >= 0 && kv < kb) inv[atomicAdd(&cur[kv], 1)] = e / topk;
+  }
+}
+
+__global__ __launch_bounds__(256) void csr_sort_kernel(const int32_t* __restrict__ counts,
+                                                        const int32_t* __restrict__ offsets,
+                                                        int32_t* __restrict__ inverse, int qb,
+                                                        int kb, int topk) {
+  extern __shared__ int ismem[];
+  int* hist = ismem;     // qb
+  int* tmp = hist + qb;  // 256
+  const int64_t b = blockIdx.y;
+  const int kv = blockIdx.x;
+  const int len = counts[b * kb + kv];
+  if (len <= 1) return;  // uniform across the workgroup
+  int32_t* seg = inverse + b * (int64_t)qb * topk + offsets[b * kb + kv];
+  for (int i = threadIdx.x; i < qb; i += 256) hist[i] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < len; i += 256) atomicAdd(&hist[seg[i]], 1);
+  __syncthreads();
+  block_exclusive_scan(hist, qb, tmp);  // hist[q] -> first slot of q
+  for (int qid = threadIdx.x; qid < qb; qid += 256) {
+    const int start = hist[qid];
+    const int end = qid + 1 < qb ? hist[qid + 1] : len;
+    for (int r = start; r < end; ++r) seg[r] = qid;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward preprocessing: one workgroup per (bh, query block).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(
+    const T* __restrict__ out, const T* __restrict__ dout, const T* __restrict__ outc,
+    const T* __restrict__ gate, int gate_mode, float* __restrict__ delta,
+    T* __restrict__ d_outc, T* __restrict__ d_gate, int qb, int D, int be) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float part[256 * VEC];
+  const int64_t blk = blockIdx.x + (int64_t)blockIdx.y * qb;  // bh*qb + n
+  const int tpr = D / VEC, rpi = 256 / tpr;
+  const int col = threadIdx.x % tpr, row0 = threadIdx.x / tpr;
+  const int c0 = col * VEC;
+  float oc[VEC], dacc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    oc[e] = outc ? Elem<T>::to_f(outc[blk * D + c0 + e]) : 0.f;
+    dacc[e] = 0.f;
+  }
+  for (int t = row0; t < be; t += rpi) {
+    const int64_t tok = blk * be + t;
+    const int64_t off = tok * D + c0;
+    u32x4 ro = *reinterpret_cast<const u32x4*>(out + off);
+    u32x4 rd = *reinterpret_cast<const u32x4*>(dout + off);
+    const T* o = reinterpret_cast<const T*>(&ro);
+    const T* g = reinterpret_cast<const T*>(&rd);
+    float gv[VEC];
+    if (gate_mode == 1) {
+      u32x4 rg = *reinterpret_cast<const u32x4*>(gate + off);
+      const T* gg = reinterpret_cast<const T*>(&rg);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) gv[e] = Elem<T>::to_f(gg[e]);
+    } else {
+      const float gs = gate_mode == 2 ? Elem<T>::to_f(gate[tok]) : 1.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) gv[e] = gs;
+    }
+    float dl = 0.f, dg = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float dov = Elem<T>::to_f(g[e]);
+      const float attn = outc ? Elem<T>::to_f(o[e]) - oc[e] * gv[e] : Elem<T>::to_f(o[e]);
+      dl = fmaf(attn, dov, dl);
+      if (outc) {
+        dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[e]);
+        if (gate_mode == 1)
+          d_gate[off + e] = Elem<T>::from_f(dov * oc[e]);
+        else
+          dg = fmaf(dov, oc[e], dg);
+      }
+    }
+    // reduce over the tpr lanes of this row (contiguous lanes)
+    for (int o2 = tpr >> 1; o2 > 0; o2 >>= 1) {
+      dl += __shfl_xor(dl, o2, 64);
+      dg += __shfl_xor(dg, o2, 64);
+    }
+    if (col == 0) {
+      delta[tok] = dl;
+      if (outc && gate_mode == 2) d_gate[tok] = Elem<T>::from_f(dg);
+    }
+  }
+  if (outc) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) part[row0 * D + c0 + e] = dacc[e];
+    __syncthreads();
+    for (int d = threadIdx.x; d < D; d += 256) {
+      float s = 0.f;
+      for (int r = 0; r < rpi; ++r) s += part[r * D + d];
+      d_outc[blk * D + d] = Elem<T>::from_f(s);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Coarse backward.  Pass A (one workgroup per (bh, q row)): dP, softmax
+// backward, scale, d_q_c.  Pass B (one workgroup per (bh, kv row)): d_k_c, d_v_c.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void coarse_bwd_rows_kernel(
+    const T* __restrict__ kc, const T* __restrict__ vc, const float* __restrict__ probs,
+    const T* __restrict__ d_outc, float* __restrict__ ds, T* __restrict__ d_qc, int qb, int kb,
+    int D, float scale) {
+  extern __shared__ float smem[];
+  float* grow = smem;        // D
+  float* dsrow = grow + D;   // kb
+  float* red = dsrow + kb;   // 4
+  const int64_t b = blockIdx.y;
+  const int i = blockIdx.x;
+  const int64_t rowq = b * qb + i;
+  for (int d = threadIdx.x; d < D; d += 256) grow[d] = Elem<T>::to_f(d_outc[rowq * D + d]);
+  __syncthreads();
+  const T* vbase = vc + b * kb * (int64_t)D;
+  const float* prow = probs + rowq * kb;
+  float lsum = 0.f;
+  for (int j = threadIdx.x; j < kb; j += 256) {
+    const T* vr = vbase + (int64_t)j * D;
+    float dot = 0.f;
+    for (int d = 0; d < D; ++d) dot = fmaf(grow[d], Elem<T>::to_f(vr[d]), dot);
+    const float dp = round_t<T>(dot);
+    dsrow[j] = dp;
+    lsum = fmaf(prow[j], dp, lsum);
+  }
+  const float sum = block_reduce<false>(lsum, red);
+  for (int j = threadIdx.x; j < kb; j += 256) {
+    const float p = prow[j];
+    const float dsv = round_t<T>(round_t<T>(p * (dsrow[j] - sum)) * scale);
+    dsrow[j] = dsv;
+    ds[rowq * kb + j] = dsv;
+  }
+  __syncthreads();
+  const T* kbase = kc + b * kb * (int64_t)D;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < kb; ++j) acc = fmaf(dsrow[j], Elem<T>::to_f(kbase[(int64_t)j * D + d]), acc);
+    d_qc[rowq * D + d] = Elem<T>::from_f(acc);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coarse_bwd_cols_kernel(
+    const T* __restrict__ qc, const float* __restrict__ probs, const T* __restrict__ d_outc,
+    const float* __restrict__ ds, T* __restrict__ d_kc, T* __restrict__ d_vc, int qb, int kb,
+    int D) {
+  const int64_t b = blockIdx.y;
+  const int j = blockIdx.x;
+  const T* qbase = qc + b * qb * (int64_t)D;
+  const T* gbase = d_outc + b * qb * (int64_t)D;
+  const float* dsb = ds + b * qb * (int64_t)kb;
+  const float* pb = probs + b * qb * (int64_t)kb;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float ak = 0.f, av = 0.f;
+    for (int i = 0; i < qb; ++i) {
+      ak = fmaf(dsb[(int64_t)i * kb + j], Elem<T>::to_f(qbase[(int64_t)i * D + d]), ak);
+      av = fmaf(pb[(int64_t)i * kb + j], Elem<T>::to_f(gbase[(int64_t)i * D + d]), av);
+    }
+    d_kc[(b * kb + j) * D + d] = Elem<T>::from_f(ak);
+    d_vc[(b * kb + j) * D + d] = Elem<T>::from_f(av);
+  }
+}
+
+}  // namespace vsa
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+using namespace vsa;
+
+extern "C" const char* vsa_status_string(int status) {
+  switch (status) {
+    case VSA_OK: return "ok";
+    case VSA_ERR_NULL: return "a required pointer is NULL";
+    case VSA_ERR_SHAPE: return "sizes are inconsistent or out of range";
+    case VSA_ERR_DTYPE: return "dtype not supported by this entry point";
+    case VSA_ERR_UNSUPPORTED: return "no kernel for this (block_elements, head_dim) pair";
+    case VSA_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+extern "C" const char* vsa_version(void) { return "mi355x-vsa 0.1 (gfx950)"; }
+
+static bool vec_dim_ok(int D, int dtype) {
+  const int vec = dtype == VSA_F32 ? 4 : 8;
+  if (D <= 0 || D % vec) return false;
+  const int tpr = D / vec;
+  return tpr <= 256 && (256 % tpr) == 0;
+}
+
+extern "C" int vsa_pool_qkv(const void* q, const void* k, const void* v, const int32_t* q_vbs,
+                            const int32_t* kv_vbs, void* q_c, void* k_c, void* v_c, int64_t bh,
+                            int64_t sq, int64_t skv, int32_t D, int32_t be, int32_t dtype,
+                            void* stream) {
+  if (!q || !k || !v || !q_vbs || !kv_vbs || !q_c || !k_c || !v_c) return VSA_ERR_NULL;
+  if (bh <= 0 || be <= 0 || sq <= 0 || skv <= 0 || sq % be || skv % be || !vec_dim_ok(D, dtype))
+    return VSA_ERR_SHAPE;
+  const int qb = (int)(sq / be), kb = (int)(skv / be);
+  const int64_t grid = bh * (qb + 2 * (int64_t)kb);
+  hipStream_t s = (hipStream_t)stream;
+  VSA_DISPATCH_ALL(dtype, T, {
+    hipLaunchKernelGGL(pool_qkv_kernel<T>, dim3((unsigned)grid), dim3(256), 0, s, (const T*)q,
+                       (const T*)k, (const T*)v, q_vbs, kv_vbs, (T*)q_c, (T*)k_c, (T*)v_c, bh, qb,
+                       kb, D, be);
+  });
+  return vsa_check_launch();
+}
+
+extern "C" int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c, float* scores,
+                              float* probs, void* out_c, int32_t* selected, int64_t bh,
+                              int32_t qb, int32_t kb, int32_t D, int32_t topk, float scale,
+                              int32_t dtype, void* stream) {
+  if (!q_c || !k_c || !v_c || !scores || !probs || !out_c) return VSA_ERR_NULL;
+  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
+    return VSA_ERR_SHAPE;
+  if (selected && (topk < 1 || topk > kb)) return VSA_ERR_SHAPE;
+  const size_t shm = (size_t)(D + 2 * kb + 4) * sizeof(float) + 256 * sizeof(int);
+  hipStream_t s = (hipStream_t)stream;
+  VSA_DISPATCH_ALL(dtype, T, {
+    hipLaunchKernelGGL(coarse_fwd_kernel<T>, dim3(qb, (unsigned)bh), dim3(256), shm, s,
+                       (const T*)q_c, (const T*)k_c, (const T*)v_c, scores, probs, (T*)out_c,
+                       selected, qb, kb, D, topk, scale);
+  });
+  return vsa_check_launch();
+}
+
+extern "C" int vsa_topk(const float* scores, int32_t* selected, int64_t rows, int32_t kb,
+                        int32_t topk, void* stream) {
+  if (!scores || !selected) return VSA_ERR_NULL;
+  if (rows <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || topk < 1 || topk > kb) return VSA_ERR_SHAPE;
+  const size_t shm = (size_t)kb * sizeof(float) + 256 * sizeof(int);
+  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(256), shm, (hipStream_t)stream,
+                     scores, selected, kb, topk);
+  return vsa_check_launch();
+}
+
+constexpr int kMaxCsrBlocks = 8064;  // 2*Kb + 256 ints of LDS stay under 64 KiB
+
+extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
+                             int32_t* inverse, int64_t bh, int32_t qb, int32_t kb, int32_t topk,
+                             void* stream) {
+  if (!selected || !counts || !offsets || !inverse) return VSA_ERR_NULL;
+  if (bh <= 0 || qb <= 0 || kb <= 0 || topk <= 0 || kb > kMaxCsrBlocks || qb > kMaxCsrBlocks ||
+      (int64_t)qb * topk > (1 << 30))
+    return VSA_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(csr_scatter_kernel, dim3((unsigned)bh), dim3(256),
+                     (size_t)(2 * kb + 256) * sizeof(int), s, selected, counts, offsets, inverse,
+                     qb, kb, topk);
+  int rc = vsa_check_launch();
+  if (rc) return rc;
+  hipLaunchKernelGGL(csr_sort_kernel, dim3(kb, (unsigned)bh), dim3(256),
+                     (size_t)(qb + 256) * sizeof(int), s, counts, offsets, inverse, qb, kb, topk);
+  return vsa_check_launch();
+}
+
+extern "C" int vsa_bwd_prep(const void* out, const void* dout, const void* out_c,
+                            const void* gate, int32_t gate_mode, float* delta, void* d_out_c,
+                            void* d_gate, int64_t bh, int64_t sq, int32_t D, int32_t be,
+                            int32_t dtype, void* stream) {
+  if (!out || !dout || !delta) return VSA_ERR_NULL;
+  if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;
+  if (out_c && !d_out_c) return VSA_ERR_NULL;
+  if (out_c && gate_mode != 0 && (!gate || !d_gate)) return VSA_ERR_NULL;
+  if (!out_c) gate_mode = 0;
+  if (bh <= 0 || be <= 0 || sq <= 0 || sq % be || !vec_dim_ok(D, dtype)) return VSA_ERR_SHAPE;
+  const int qb = (int)(sq / be);
+  hipStream_t s = (hipStream_t)stream;
+  VSA_DISPATCH_ALL(dtype, T, {
+    hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3(qb, (unsigned)bh), dim3(256), 0, s,
+                       (const T*)out, (const T*)dout, (const T*)out_c, (const T*)gate, gate_mode,
+                       delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
+  });
+  return vsa_check_launch();
+}
+
+extern "C" int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c,
+                              const float* probs, const void* d_out_c, float* ds, void* d_q_c,
+                              void* d_k_c, void* d_v_c, int64_t bh, int32_t qb, int32_t kb,
+                              int32_t D, float scale, int32_t dtype, void* stream) {
+  if (!q_c || !k_c || !v_c || !probs || !d_out_c || !ds || !d_q_c || !d_k_c || !d_v_c)
+    return VSA_ERR_NULL;
+  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
+    return VSA_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t shm = (size_t)(D + kb + 4) * sizeof(float);
+  int rc = 0;
+  VSA_DISPATCH_ALL(dtype, T, {
+    hipLaunchKernelGGL(coarse_bwd_rows_kernel<T>, dim3(qb, (unsigned)bh), dim3(256), shm, s,
+                       (const T*)k_c, (const T*)v_c, probs, (const T*)d_out_c, ds, (T*)d_q_c, qb,
+                       kb, D, scale);
+    rc = vsa_check_launch();
+    if (rc == 0)
+      hipLaunchKernelGGL(coarse_bwd_cols_kernel<T>, dim3(kb, (unsigned)bh), dim3(256), 0, s,
+                         (const T*)q_c, probs, (const T*)d_out_c, ds, (T*)d_k_c, (T*)d_v_c, qb,
+                         kb, D);
+  });
+  if (rc) return rc;
+  return vsa_check_launch();
+}

@@ -1,0 +1,328 @@
+// Sparse fine forward on gfx950 MFMA, with the combine fused into the epilogue.
+//
+// Reference contract: _triton_sparse_attention_forward (triton_impl.py:358-473)
+// and its kernels (39-355); combine: fused_common.py:175-199.
+//
+// Work decomposition: one workgroup owns QT query rows of one (b, h) (QT = 128
+// for block volume >= 128, else the block), one wave owns 32 of them.  The
+// workgroup walks the selected KV blocks of its query block in 64-key chunks;
+// every chunk is staged in LDS once (K row-major, V transposed) and shared by
+// all waves; the next chunk's global loads are in flight while the current
+// chunk is multiplied (double-buffered LDS, one barrier per chunk).
+//
+// Per wave and chunk:
+//   S^T (64 x 32)  = K (64 x D) . Q^T (D x 32)           A = K from LDS, B = Q in VGPRs
+//   online softmax per query (each lane owns one query: column r of S^T)
+//   O^T (D x 32)  += V^T (D x 64) . P^T (64 x 32)        A = V^T from LDS, B = P in VGPRs
+// Holding S and O transposed keeps the softmax statistics and the O rescale
+// lane-local; only the row max crosses the two lane halves.
+#include "vsa_device.h"
+#include "vsa_launch.h"
+
+namespace vsa {
+
+template <int D, int BE>
+struct FwdCfg {
+  static constexpr int QT = BE >= 128 ? 128 : BE;  // queries per workgroup
+  static constexpr int NW = QT / 32;               // waves per workgroup
+  static constexpr int NT = NW * 64;
+  static constexpr int KC = 64;                    // keys per chunk
+  static constexpr int KP = D + 8;                 // K row pitch (elements)
+  static constexpr int VP = KC + 8;                // V^T row pitch (elements)
+  static constexpr int KS = KC * KP;
+  static constexpr int VS = D * VP;
+  static constexpr int STAGE = KS + VS;
+  static constexpr int K_PIECES = KC * D / 8;      // 16-byte pieces of a K chunk
+  static constexpr int K_PER_T = (K_PIECES + NT - 1) / NT;
+  static constexpr int V_UNITS = (KC / 4) * (D / 8);  // 4 keys x 8 dims per unit
+  static constexpr int V_PER_T = (V_UNITS + NT - 1) / NT;
+  static constexpr int NCHUNK = BE / KC;
+};
+
+// Advance (slot, chunk) to the next chunk that holds at least one valid key.
+template <int BE>
+__device__ __forceinline__ bool next_valid_chunk(const int32_t* __restrict__ sel,
+                                                 const int32_t* __restrict__ vbs, int topk,
+                                                 int kb, int& s, int& c, int& kv, int& nvb) {
+  while (s < topk) {
+    kv = sel[s];
+    if (kv >= 0 && kv < kb) {
+      nvb = clamp_valid(vbs[kv], BE);
+      if (c * 64 < nvb) return true;
+    }
+    ++s;
+    c = 0;
+  }
+  return false;
+}
+
+template <typename T, int D, int BE>
+__global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void sparse_fwd_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
+    T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
+    const T* __restrict__ gate, int gate_mode, int num_tiles, int tiles_per_head, int sq,
+    int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
+  using C = FwdCfg<D, BE>;
+  using E = Elem<T>;
+  typedef typename E::vec8 V8;
+  __shared__ __attribute__((aligned(16))) T smem[2 * C::STAGE];
+
+  const int tile = xcd_tile(blockIdx.x, num_tiles);
+  if (tile >= num_tiles) return;
+  const int64_t b = tile / tiles_per_head;
+  const int q0 = (tile % tiles_per_head) * C::QT;
+  const int qblk = q0 / BE;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r = lane & 31, h = lane >> 5;
+  const int myq = q0 + wave * 32 + r;
+
+  // Q^T fragments: lane (r, h) holds query r, dims 16*ks + 8h .. +7.
+  V8 qf[D / 16];
+  {
+    const T* qrow = q + ((int64_t)b * sq + myq) * D + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + 16 * ks);
+      raw ^= qsign;  // negative softmax scale folded into q
+      qf[ks] = as_vec8<T>(raw);
+    }
+  }
+
+  const int32_t* sel = selected + ((int64_t)b * qb + qblk) * topk;
+  const T* kbase = k + (int64_t)b * skv * D;
+  const T* vbase = v + (int64_t)b * skv * D;
+
+  u32x4 kreg[C::K_PER_T];
+  u32x4 vreg[C::V_PER_T][4];
+  auto gload = [&](int kvb, int ch) {
+    const int64_t off = ((int64_t)kvb * BE + ch * C::KC) * D;
+    const T* kp = kbase + off;
+    const T* vp = vbase + off;
+#pragma unroll
+    for (int i = 0; i < C::K_PER_T; ++i) {
+      const int p = tid + i * C::NT;
+      if (C::K_PIECES % C::NT == 0 || p < C::K_PIECES)
+        kreg[i] = *reinterpret_cast<const u32x4*>(kp + p * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < C::V_PER_T; ++i) {
+      const int u = tid + i * C::NT;
+      if (C::V_UNITS % C::NT == 0 || u < C::V_UNITS) {
+        const int kg = u & 15, dg = u >> 4;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          vreg[i][rr] = *reinterpret_cast<const u32x4*>(vp + (kg * 4 + rr) * D + dg * 8);
+      }
+    }
+  };
+  auto lstore = [&](int stage) {
+    T* Ks = smem + stage * C::STAGE;
+    T* Vt = Ks + C::KS;
+#pragma unroll
+    for (int i = 0; i < C::K_PER_T; ++i) {
+      const int p = tid + i * C::NT;
+      if (C::K_PIECES % C::NT == 0 || p < C::K_PIECES) {
+        const int key = p / (D / 8), dc = p % (D / 8);
+        *reinterpret_cast<u32x4*>(Ks + key * C::KP + dc * 8) = kreg[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::V_PER_T; ++i) {
+      const int u = tid + i * C::NT;
+      if (C::V_UNITS % C::NT == 0 || u < C::V_UNITS) {
+        const int kg = u & 15, dg = u >> 4;
+        u32x2 cols[8];
+        transpose4x8_b16(vreg[i], cols);
+        const int pos = (kg >> 2) * 16 + group4_pos(kg & 3) * 4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<u32x2*>(Vt + (dg * 8 + j) * C::VP + pos) = cols[j];
+      }
+    }
+  };
+
+  float m = -INFINITY;  // running max in log2 units (scaled)
+  float lsum = 0.f;     // per-lane partial row sum
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) oacc[mt] = f32x16{};
+
+  int s = 0, ch = 0, kv = 0, nvb = 0;
+  bool have = next_valid_chunk<BE>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
+  if (have) {
+    gload(kv, ch);
+    lstore(0);
+  }
+  __syncthreads();
+  int stage = 0;
+  while (have) {
+    const int nv = min(nvb - ch * 64, 64);
+    int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
+    const bool have2 = next_valid_chunk<BE>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
+    if (have2) gload(kv2, ch2);
+
+    const T* Ks = smem + stage * C::STAGE;
+    const T* Vt = Ks + C::KS;
+    // ---- S^T = K Q^T -------------------------------------------------------
+    f32x16 sacc[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+#pragma unroll
+      for (int smt = 0; smt < 2; ++smt) {
+        const V8 a = as_vec8<T>(
+            *reinterpret_cast<const u32x4*>(Ks + (smt * 32 + r) * C::KP + ks * 16 + h * 8));
+        sacc[smt] = E::mfma32(a, qf[ks], sacc[smt]);
+      }
+    }
+    // ---- online softmax (base 2) ------------------------------------------
+    float smax = -INFINITY;
+    if (nv < 64) {
+#pragma unroll
+      for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (key >= nv) sacc[smt][i] = -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) smax = fmaxf(smax, sacc[smt][i]);
+    smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+    const float mnew = fmaxf(m, smax * c2);
+    if (__any(mnew > m)) {  // exact: alpha == 1 where the max did not move
+      const float alpha = exp2f(m - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt) oacc[mt] *= alpha;
+      m = mnew;
+    }
+    float p[2][16];
+    const float negm = -m;
+#pragma unroll
+    for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        p[smt][i] = exp2f(fmaf(sacc[smt][i], c2, negm));
+      }
+    if (nv < 64) {
+#pragma unroll
+      for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (key >= nv) p[smt][i] = 0.f;
+        }
+    }
+#pragma unroll
+    for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) lsum += p[smt][i];
+    // ---- O^T += V^T P^T -------------------------------------------------------
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const V8 bop = pack8<T>(&p[kk >> 1][8 * (kk & 1)]);
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt) {
+        const V8 a = as_vec8<T>(
+            *reinterpret_cast<const u32x4*>(Vt + (mt * 32 + r) * C::VP + kk * 16 + h * 8));
+        oacc[mt] = E::mfma32(a, bop, oacc[mt]);
+      }
+    }
+
+    if (have2) lstore(stage ^ 1);
+    __syncthreads();
+    stage ^= 1;
+    s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
+  }
+
+  // ---- epilogue: normalise, fused combine, LSE ----------------------------
+  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  const float inv = 1.0f / ltot;
+  const int64_t tok = (int64_t)b * sq + myq;
+  if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
+  const T* ocrow = outc ? outc + ((int64_t)b * qb + qblk) * D : nullptr;
+  float gtok = 1.f;
+  if (outc && gate_mode == 2) gtok = E::to_f(gate[tok]);
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = mt * 32 + 8 * g + 4 * h;
+      float val[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) val[e] = oacc[mt][4 * g + e] * inv;
+      if (ocrow) {
+        u32x2 ocr = *reinterpret_cast<const u32x2*>(ocrow + d0);
+        const T* oc = reinterpret_cast<const T*>(&ocr);
+        float gv[4] = {gtok, gtok, gtok, gtok};
+        if (gate_mode == 1) {
+          u32x2 gr = *reinterpret_cast<const u32x2*>(gate + tok * D + d0);
+          const T* gg = reinterpret_cast<const T*>(&gr);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) gv[e] = E::to_f(gg[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = fmaf(E::to_f(oc[e]), gv[e], val[e]);
+      }
+      T o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = E::from_f(val[e]);
+      *reinterpret_cast<u32x2*>(out + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
+    }
+  }
+}
+
+template <typename T, int D, int BE>
+static int launch_fwd(const void* q, const void* k, const void* v, const int32_t* selected,
+                      const int32_t* kv_vbs, void* out, float* lse, const void* outc,
+                      const void* gate, int gate_mode, int64_t bh, int64_t sq, int64_t skv,
+                      int topk, float scale, hipStream_t stream) {
+  using C = FwdCfg<D, BE>;
+  const int tph = (int)(sq / C::QT);
+  const int64_t tiles = bh * tph;
+  if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
+  const int grid = (int)(((tiles + 7) / 8) * 8);
+  const float c2 = fabsf(scale) * kLog2e;
+  const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
+  hipLaunchKernelGGL((sparse_fwd_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
+                     (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, lse,
+                     (const T*)outc, (const T*)gate, gate_mode, (int)tiles, tph, (int)sq,
+                     (int)skv, (int)(sq / BE), (int)(skv / BE), topk, c2, qsign);
+  return vsa_check_launch();
+}
+
+}  // namespace vsa
+
+using namespace vsa;
+
+#define VSA_FWD_CASE(DD, BB)                                                                   \
+  if (D == DD && be == BB)                                                                     \
+    return launch_fwd<T, DD, BB>(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode, \
+                                 bh, sq, skv, topk, scale, s);
+
+extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
+                              const int32_t* selected, const int32_t* kv_vbs, void* out,
+                              float* lse, const void* out_c, const void* gate, int32_t gate_mode,
+                              int64_t bh, int64_t sq, int64_t skv, int32_t D, int32_t be,
+                              int32_t topk, float scale, int32_t dtype, void* stream) {
+  if (!q || !k || !v || !selected || !kv_vbs || !out) return VSA_ERR_NULL;
+  if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;
+  if (out_c && gate_mode != 0 && !gate) return VSA_ERR_NULL;
+  if (!out_c) gate_mode = 0;
+  if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
+      sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
+    return VSA_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  VSA_DISPATCH_MFMA(dtype, T, {
+    VSA_FWD_CASE(128, 256)
+    VSA_FWD_CASE(128, 128)
+    VSA_FWD_CASE(128, 64)
+    VSA_FWD_CASE(64, 256)
+    VSA_FWD_CASE(64, 128)
+    VSA_FWD_CASE(64, 64)
+  });
+  return VSA_ERR_UNSUPPORTED;
+}

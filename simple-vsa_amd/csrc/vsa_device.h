@@ -1,0 +1,149 @@
+// Device-side helpers shared by the gfx950 VSA kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * tensors are dense row-major [B*H, S, D] (the reference's BHSD layout made
+//    contiguous, triton_impl.py:1593-1595);
+//  * fp32 accumulation everywhere, stores rounded to the element type T with
+//    round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950);
+//  * MFMA tiles are CDNA4's v_mfma_f32_32x32x16_{bf16,f16}.  For a wave with
+//    lane = 32*h + r (r in 0..31, h in 0..1):
+//       A (32 x 16, M x K): lane holds row r, k = 8h .. 8h+7
+//       B (16 x 32, K x N): lane holds col r, k = 8h .. 8h+7
+//       C (32 x 32, M x N): acc[i] is row 8*(i/4) + 4h + (i%4), col r
+//    Because a C tile's per-lane rows are {16j + 4h + 0..3, 16j + 8 + 4h + 0..3}
+//    for acc[8j .. 8j+7], a C tile converted to T can be fed straight back as
+//    the B (or A) operand of a product that reduces over the C tile's rows,
+//    provided the other operand enumerates those rows in the same order.
+//    Sequence-major operands that must be read "down a column" are therefore
+//    stored transposed in LDS with the row order permuted inside each group of
+//    16: position p holds sequence index perm16(p) (see seq_pos16 below).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vsa {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------------------
+// Element traits
+// ---------------------------------------------------------------------------
+template <typename T> struct Elem;
+
+template <> struct Elem<__bf16> {
+  typedef bf16x8 vec8;
+  static __device__ __forceinline__ float to_f(__bf16 x) { return (float)x; }
+  static __device__ __forceinline__ __bf16 from_f(float x) { return (__bf16)x; }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Elem<_Float16> {
+  typedef f16x8 vec8;
+  static __device__ __forceinline__ float to_f(_Float16 x) { return (float)x; }
+  static __device__ __forceinline__ _Float16 from_f(float x) { return (_Float16)x; }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float to_f(float x) { return x; }
+  static __device__ __forceinline__ float from_f(float x) { return x; }
+};
+
+// Round an fp32 value through T and back (the reference's "computed in fp32,
+// stored in T" points).
+template <typename T>
+__device__ __forceinline__ float round_t(float x) {
+  return Elem<T>::to_f(Elem<T>::from_f(x));
+}
+
+// Pack 8 fp32 values (two groups of 4) into an MFMA operand of T.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 pack8(const float* v) {
+  typename Elem<T>::vec8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = Elem<T>::from_f(v[e]);
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 as_vec8(u32x4 x) {
+  return __builtin_bit_cast(typename Elem<T>::vec8, x);
+}
+
+// ---------------------------------------------------------------------------
+// Transposed-tile bookkeeping.
+//   seq_pos16(s): LDS position (inside a 16-group) of sequence index s, so that
+//   lane half h reading positions 8h .. 8h+7 receives sequence indices
+//   {4h .. 4h+3, 8+4h .. 8+4h+3} -- the rows of a C tile owned by that half.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int group4_pos(int g) {  // g: 4-group inside 16
+  return ((g & 1) << 1) | ((g >> 1) & 1);
+}
+
+// Transpose a 4 (rows) x 8 (cols) block of 16-bit values held as 4 rows of
+// u32x4 into 8 rows of 4 values (u32x2 each): out[c] = {r0[c], r1[c], r2[c], r3[c]}.
+__device__ __forceinline__ void transpose4x8_b16(const u32x4 (&rows)[4], u32x2 (&out)[8]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    // low halves -> column 2m, high halves -> column 2m+1
+    uint32_t a0 = rows[0][m], a1 = rows[1][m], a2 = rows[2][m], a3 = rows[3][m];
+    out[2 * m][0] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
+    out[2 * m][1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
+    out[2 * m + 1][0] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
+    out[2 * m + 1][1] = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wave / block reductions (wave64)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide reduction through LDS; `red` must hold blockDim.x/64 floats.
+template <bool kMax>
+__device__ __forceinline__ float block_reduce(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  v = kMax ? wave_max(v) : wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < nw; ++w) r = kMax ? fmaxf(r, red[w]) : r + red[w];
+  return r;
+}
+
+__device__ __forceinline__ int clamp_valid(int32_t vbs, int be) {
+  return vbs < 0 ? 0 : (vbs > be ? be : (int)vbs);
+}
+
+// XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs
+// of an MI355X, so linear id i runs on XCD i % 8.  Give XCD x the contiguous
+// tile range [x*per, (x+1)*per) so the tiles of one head stay on one XCD's L2.
+__device__ __forceinline__ int xcd_tile(int linear_id, int num_tiles) {
+  const int per = (num_tiles + 7) >> 3;
+  return (linear_id & 7) * per + (linear_id >> 3);
+}
+
+}  // namespace vsa

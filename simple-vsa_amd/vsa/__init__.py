@@ -1,0 +1,30 @@
+"""MI355X-native Video Sparse Attention.
+
+Importing ``vsa`` needs only torch; the gfx950 kernel library is loaded on the
+first call, as the reference loads its GPU backends (vsa/__init__.py:28-69).
+"""
+
+from typing import Any
+
+__all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_route"]
+
+
+def mi355x_vsa(*args: Any, **kwargs: Any) -> Any:
+    """Full VSA (coarse + routed fine branch) on MI355X; see ``vsa.mi355x``."""
+    from .mi355x import mi355x_vsa as _impl
+
+    return _impl(*args, **kwargs)
+
+
+def mi355x_sparse_attention(*args: Any, **kwargs: Any) -> Any:
+    """Route-explicit sparse executor on MI355X; see ``vsa.mi355x``."""
+    from .mi355x import mi355x_sparse_attention as _impl
+
+    return _impl(*args, **kwargs)
+
+
+def mi355x_route(*args: Any, **kwargs: Any) -> Any:
+    """Coarse scores and Top-K route that ``mi355x_vsa`` uses."""
+    from .mi355x import mi355x_route as _impl
+
+    return _impl(*args, **kwargs)

@@ -1,0 +1,346 @@
+"""Host orchestration of the MI355X VSA path (Python over the gfx950 C ABI).
+
+Public entry points keep the reference's operator API:
+
+* ``mi355x_vsa(q, k, v, variable_block_sizes, q_variable_block_sizes, topk,
+  block_size=64, compress_attn_weight=None)`` -- drop-in for ``torch_vsa`` /
+  ``triton_vsa`` (torch_impl.py:49-57, triton_impl.py:1734-1765);
+* ``mi355x_sparse_attention(q, k, v, selected, variable_block_sizes, *,
+  block_size, sm_scale=None)`` -- drop-in for ``triton_sparse_attention``
+  (triton_impl.py:1626-1652).
+
+Both are differentiable (one ``torch.autograd.Function`` each).  Every
+compute step is a HIP kernel behind ``_lib``; the host only validates,
+allocates outputs/workspace with ``torch.empty`` and launches on the current
+stream, with no device synchronisation.
+
+The building blocks (pooling, coarse attention + Top-K, CSR inversion, fine
+forward / backward) are exposed as functions so tests can check each kernel.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple, Union
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+SUPPORTED_BLOCKS = (64, 128, 256)
+SUPPORTED_HEAD_DIMS = (64, 128)
+MFMA_DTYPES = (torch.bfloat16, torch.float16)
+
+
+# ---------------------------------------------------------------------------
+# Validation (texts follow common.py:97-134 and triton_impl.py:371-401)
+# ---------------------------------------------------------------------------
+
+def as_block_elements(block_size: Union[int, Tuple[int, ...]]) -> int:
+    """Block volume: int -> cube, tuple -> product (common.py:39-42)."""
+    if isinstance(block_size, int):
+        return block_size * block_size * block_size
+    return int(math.prod(block_size))
+
+
+def validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk,
+                        block_elements) -> None:
+    """Shape contract of ``video_sparse_attn`` (common.py:97-134)."""
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must have shape [batch, heads, seq_len, dim]")
+    batch, heads, q_len, dim = q.shape
+    kv_len = k.shape[2]
+    if k.shape[0] != batch or v.shape[0] != batch or k.shape[1] != heads or v.shape[1] != heads:
+        raise ValueError("q, k, and v must share batch and head dimensions")
+    if v.shape[2] != kv_len:
+        raise ValueError("k and v must have the same sequence length")
+    if k.shape[-1] != dim or v.shape[-1] != dim:
+        raise ValueError("q, k, and v must have the same head dimension")
+    if q_len % block_elements or kv_len % block_elements:
+        raise ValueError(
+            f"q/kv sequence lengths must be divisible by block_elements={block_elements}")
+    qb, kb = q_len // block_elements, kv_len // block_elements
+    if variable_block_sizes.numel() != kb:
+        raise ValueError(
+            f"variable_block_sizes must have length {kb}, got {variable_block_sizes.numel()}")
+    if q_variable_block_sizes.numel() != qb:
+        raise ValueError(
+            f"q_variable_block_sizes must have length {qb}, got {q_variable_block_sizes.numel()}")
+    if not 1 <= topk <= kb:
+        raise ValueError(f"topk must be in [1, {kb}]")
+
+
+def _check_device_path(q, k, v, block_elements) -> None:
+    """Constraints of the gfx950 kernels (the reference's GPU checks,
+    triton_impl.py:371-384, narrowed to the shapes that have MI355X kernels)."""
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("the MI355X implementation requires GPU tensors")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, and v must be on the same GPU device")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, and v must have the same dtype")
+    if q.dtype not in MFMA_DTYPES:
+        raise ValueError("the MI355X kernels support float16 and bfloat16")
+    if block_elements not in SUPPORTED_BLOCKS:
+        raise ValueError(f"the MI355X kernels support block_size volumes {SUPPORTED_BLOCKS}")
+    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"the MI355X kernels support head_dim in {SUPPORTED_HEAD_DIMS}")
+
+
+def _i32(x: Tensor, device) -> Tensor:
+    return x.to(device=device, dtype=torch.int32).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Kernel-level building blocks (each one C-ABI call)
+# ---------------------------------------------------------------------------
+
+def block_mean_qkv(q, k, v, variable_block_sizes, q_variable_block_sizes, block_elements):
+    """Pooled ``(q_c, k_c, v_c)`` in the input dtype (fused_block_mean x3)."""
+    b, h, sq, d = q.shape
+    skv = k.shape[2]
+    qc = torch.empty((b, h, sq // block_elements, d), device=q.device, dtype=q.dtype)
+    kc = torch.empty((b, h, skv // block_elements, d), device=q.device, dtype=q.dtype)
+    vc = torch.empty_like(kc)
+    _lib.call("vsa_pool_qkv", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
+              _lib.ptr(_i32(q_variable_block_sizes, q.device)),
+              _lib.ptr(_i32(variable_block_sizes, q.device)),
+              _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), b * h, sq, skv, d, block_elements,
+              _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    return qc, kc, vc
+
+
+def coarse_forward(qc, kc, vc, topk: Optional[int], scale: float):
+    """Coarse scores / probabilities (fp32 holding T-rounded values), compact
+    ``out_c`` and, if ``topk``, the routed key blocks (int32, ascending)."""
+    b, h, qb, d = qc.shape
+    kb = kc.shape[2]
+    scores = torch.empty((b, h, qb, kb), device=qc.device, dtype=torch.float32)
+    probs = torch.empty_like(scores)
+    outc = torch.empty_like(qc)
+    sel = (torch.empty((b, h, qb, topk), device=qc.device, dtype=torch.int32)
+           if topk else None)
+    _lib.call("vsa_coarse_fwd", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(scores),
+              _lib.ptr(probs), _lib.ptr(outc), _lib.ptr(sel), b * h, qb, kb, d, topk or 0,
+              float(scale), _lib.dtype_code(qc.dtype), _lib.stream_of(qc))
+    return scores, probs, outc, sel
+
+
+def topk(scores: Tensor, k: int) -> Tensor:
+    """Top-K over the last dim of fp32 scores: ties go to the smaller id; ids
+    in ascending order (the routing rule of ``coarse_forward``)."""
+    scores = scores.contiguous().float()
+    kb = scores.shape[-1]
+    rows = scores.numel() // kb
+    out = torch.empty((*scores.shape[:-1], k), device=scores.device, dtype=torch.int32)
+    _lib.call("vsa_topk", _lib.ptr(scores), _lib.ptr(out), rows, kb, k, _lib.stream_of(scores))
+    return out
+
+
+def invert_routes(selected: Tensor, key_blocks: int):
+    """``(inverse, offsets, counts)`` CSR of ``selected`` (triton_impl.py:544-595),
+    each segment in ascending query-block order."""
+    selected = _i32(selected, selected.device)
+    b, h, qb, tk = selected.shape
+    counts = torch.empty((b, h, key_blocks), device=selected.device, dtype=torch.int32)
+    offsets = torch.empty_like(counts)
+    inverse = torch.empty((b, h, qb * tk), device=selected.device, dtype=torch.int32)
+    _lib.call("vsa_csr_build", _lib.ptr(selected), _lib.ptr(counts), _lib.ptr(offsets),
+              _lib.ptr(inverse), b * h, qb, key_blocks, tk, _lib.stream_of(selected))
+    return inverse, offsets, counts
+
+
+def sparse_forward(q, k, v, selected, variable_block_sizes, block_elements, scale, *,
+                   out_c=None, gate=None, want_lse=True):
+    """Fine forward (+ combine when ``out_c`` is given).  Returns (out, lse)."""
+    b, h, sq, d = q.shape
+    skv = k.shape[2]
+    out = torch.empty_like(q)
+    lse = (torch.empty((b, h, sq), device=q.device, dtype=torch.float32) if want_lse else None)
+    gmode = _lib.GATE_NONE if (out_c is None or gate is None) else (
+        _lib.GATE_PER_TOKEN if gate.shape[-1] == 1 and d != 1 else _lib.GATE_FULL)
+    _lib.call("vsa_sparse_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(selected),
+              _lib.ptr(variable_block_sizes), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(out_c),
+              _lib.ptr(gate if gmode else None), gmode, b * h, sq, skv, d, block_elements,
+              selected.shape[-1], float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    return out, lse
+
+
+def backward_prep(out, dout, block_elements, *, out_c=None, gate=None):
+    """delta (fp32) and, with the combine, (d_out_c, d_gate)."""
+    b, h, sq, d = out.shape
+    delta = torch.empty((b, h, sq), device=out.device, dtype=torch.float32)
+    d_outc = torch.empty_like(out_c) if out_c is not None else None
+    gmode = _lib.GATE_NONE if (out_c is None or gate is None) else (
+        _lib.GATE_PER_TOKEN if gate.shape[-1] == 1 and d != 1 else _lib.GATE_FULL)
+    d_gate = torch.empty_like(gate) if gmode else None
+    _lib.call("vsa_bwd_prep", _lib.ptr(out), _lib.ptr(dout), _lib.ptr(out_c),
+              _lib.ptr(gate if gmode else None), gmode, _lib.ptr(delta), _lib.ptr(d_outc),
+              _lib.ptr(d_gate), b * h, sq, d, block_elements, _lib.dtype_code(out.dtype),
+              _lib.stream_of(out))
+    return delta, d_outc, d_gate
+
+
+def coarse_backward(qc, kc, vc, probs, d_outc, scale):
+    b, h, qb, d = qc.shape
+    kb = kc.shape[2]
+    ds = torch.empty_like(probs)
+    dqc, dkc, dvc = torch.empty_like(qc), torch.empty_like(kc), torch.empty_like(vc)
+    _lib.call("vsa_coarse_bwd", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(probs),
+              _lib.ptr(d_outc), _lib.ptr(ds), _lib.ptr(dqc), _lib.ptr(dkc), _lib.ptr(dvc),
+              b * h, qb, kb, d, float(scale), _lib.dtype_code(qc.dtype), _lib.stream_of(qc))
+    return dqc, dkc, dvc
+
+
+def sparse_backward(q, k, v, dout, lse, delta, selected, variable_block_sizes, block_elements,
+                    scale, *, dqc=None, dkc=None, dvc=None, q_variable_block_sizes=None):
+    """dQ (query-owned) then dK/dV (KV-owned over the CSR route)."""
+    b, h, sq, d = q.shape
+    skv = k.shape[2]
+    kb = skv // block_elements
+    tk = selected.shape[-1]
+    inverse, offsets, counts = invert_routes(selected, kb)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    code, stream = _lib.dtype_code(q.dtype), _lib.stream_of(q)
+    _lib.call("vsa_sparse_bwd_dq", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(dout),
+              _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(selected), _lib.ptr(variable_block_sizes),
+              _lib.ptr(dq), _lib.ptr(dqc), _lib.ptr(q_variable_block_sizes), b * h, sq, skv, d,
+              block_elements, tk, float(scale), code, stream)
+    _lib.call("vsa_sparse_bwd_dkdv", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(dout),
+              _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(counts), _lib.ptr(offsets),
+              _lib.ptr(inverse), _lib.ptr(variable_block_sizes), _lib.ptr(dk), _lib.ptr(dv),
+              _lib.ptr(dkc), _lib.ptr(dvc), b * h, sq, skv, d, block_elements, tk, float(scale),
+              code, stream)
+    return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# Explicit-route executor (triton_impl.py:1530-1652)
+# ---------------------------------------------------------------------------
+
+class _SparseAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, selected, vbs, block_elements, scale):
+        out, lse = sparse_forward(q, k, v, selected, vbs, block_elements, scale, want_lse=True)
+        ctx.save_for_backward(q, k, v, out, lse, selected, vbs)
+        ctx.block_elements, ctx.scale = block_elements, scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, selected, vbs = ctx.saved_tensors
+        dout = dout.contiguous()
+        delta, _, _ = backward_prep(out, dout, ctx.block_elements)
+        dq, dk, dv = sparse_backward(q, k, v, dout, lse, delta, selected, vbs,
+                                     ctx.block_elements, ctx.scale)
+        return dq, dk, dv, None, None, None, None
+
+
+def _validate_route(q, k, selected, variable_block_sizes, be):
+    batch, heads, sq, _ = q.shape
+    qb, kb = sq // be, k.shape[-2] // be
+    if sq % be or k.shape[-2] % be:
+        raise ValueError(f"q/kv sequence lengths must be divisible by block_elements={be}")
+    if tuple(selected.shape[:3]) != (batch, heads, qb) or selected.ndim != 4:
+        raise ValueError("selected must have shape [batch, heads, query_blocks, topk]")
+    if not 1 <= selected.shape[-1] <= kb:
+        raise ValueError(f"selected topk must be in [1, {kb}]")
+    if variable_block_sizes.numel() != kb:
+        raise ValueError(
+            f"variable_block_sizes must have {kb} entries, got {variable_block_sizes.numel()}")
+
+
+def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
+                            variable_block_sizes: Tensor, *, block_size, sm_scale=None) -> Tensor:
+    """Sparse fine attention on a caller-supplied route ``selected``
+    ``[B, H, Qb, topk]`` (any integer dtype).  Route ids outside ``[0, Kb)``
+    contribute nothing."""
+    be = as_block_elements(block_size)
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must have shape [batch, heads, seq_len, dim]")
+    _check_device_path(q, k, v, be)
+    _validate_route(q, k, selected, variable_block_sizes, be)
+    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    selected = _i32(selected, q.device)
+    vbs = _i32(variable_block_sizes, q.device)
+    with torch.cuda.device(q.device):
+        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+            return _SparseAttention.apply(q, k, v, selected, vbs, be, float(scale))
+        return sparse_forward(q, k, v, selected, vbs, be, scale, want_lse=False)[0]
+
+
+# ---------------------------------------------------------------------------
+# Full VSA (torch_vsa / triton_vsa signature)
+# ---------------------------------------------------------------------------
+
+class _VSA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, gate, vbs, qvbs, topk_, be):
+        scale = 1.0 / math.sqrt(q.shape[-1])
+        qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
+        _, probs, outc, sel = coarse_forward(qc, kc, vc, topk_, scale)
+        out, lse = sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
+                                  want_lse=True)
+        ctx.save_for_backward(q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, out, lse)
+        ctx.be, ctx.scale = be, scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, out, lse = ctx.saved_tensors
+        dout = dout.contiguous()
+        delta, d_outc, d_gate = backward_prep(out, dout, ctx.be, out_c=outc, gate=gate)
+        dqc, dkc, dvc = coarse_backward(qc, kc, vc, probs, d_outc, ctx.scale)
+        dq, dk, dv = sparse_backward(q, k, v, dout, lse, delta, sel, vbs, ctx.be, ctx.scale,
+                                     dqc=dqc, dkc=dkc, dvc=dvc, q_variable_block_sizes=qvbs)
+        return dq, dk, dv, d_gate, None, None, None, None
+
+
+def _prepare_gate(gate: Optional[Tensor], q: Tensor) -> Optional[Tensor]:
+    if gate is None:
+        return None
+    b, h, s, d = q.shape
+    if tuple(gate.shape) not in ((b, h, s, d), (b, h, s, 1)):
+        raise ValueError(
+            "compress_attn_weight must have the same shape as q, or [batch, heads, seq_len, 1]")
+    return gate.to(device=q.device, dtype=q.dtype).contiguous()
+
+
+def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
+               q_variable_block_sizes: Tensor, topk: int, block_size=64,
+               compress_attn_weight: Optional[Tensor] = None) -> Tensor:
+    """Video Sparse Attention on MI355X: ``out = out_c * gate + out_s``
+    (torch_impl.py:49-113), coarse routing by Top-K of the pooled scores.
+
+    Top-K ties are resolved towards the smaller key-block id."""
+    be = as_block_elements(block_size)
+    validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
+    _check_device_path(q, k, v, be)
+    gate = _prepare_gate(compress_attn_weight, q)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    vbs = _i32(variable_block_sizes, q.device)
+    qvbs = _i32(q_variable_block_sizes, q.device)
+    with torch.cuda.device(q.device):
+        needs_grad = torch.is_grad_enabled() and (
+            q.requires_grad or k.requires_grad or v.requires_grad
+            or (gate is not None and gate.requires_grad))
+        if needs_grad:
+            return _VSA.apply(q, k, v, gate, vbs, qvbs, topk, be)
+        scale = 1.0 / math.sqrt(q.shape[-1])
+        qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
+        _, _, outc, sel = coarse_forward(qc, kc, vc, topk, scale)
+        return sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
+                              want_lse=False)[0]
+
+
+def mi355x_route(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, block_size=64):
+    """The routing ``mi355x_vsa`` would use: ``(scores, selected)`` with scores
+    as fp32 holding input-dtype values.  For inspection and parity tests."""
+    be = as_block_elements(block_size)
+    validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
+    qc, kc, vc = block_mean_qkv(q.contiguous(), k.contiguous(), v.contiguous(),
+                                variable_block_sizes, q_variable_block_sizes, be)
+    scores, _, _, sel = coarse_forward(qc, kc, vc, topk, 1.0 / math.sqrt(q.shape[-1]))
+    return scores, sel

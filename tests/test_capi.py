@@ -1,0 +1,93 @@
+"""CPU-side checks of the drop-in boundary: the C-ABI library loads, exports
+every entry point ``include/vsa_capi.h`` declares, reports status text, and
+the Python layer raises the reference's ValueError texts before any launch
+(tests/test_torch_vsa.py:112-130)."""
+
+import os
+import re
+
+import pytest
+import torch
+
+from vsa import _lib
+from vsa import mi355x as M
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vsa_capi.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int)\s+(vsa_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = _declared_symbols()
+    for must in ("vsa_pool_qkv", "vsa_coarse_fwd", "vsa_topk", "vsa_csr_build", "vsa_sparse_fwd",
+                 "vsa_bwd_prep", "vsa_coarse_bwd", "vsa_sparse_bwd_dq", "vsa_sparse_bwd_dkdv",
+                 "vsa_status_string", "vsa_version"):
+        assert must in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_status_strings_and_version():
+    assert _lib.status_string(0) == "ok"
+    assert "NULL" in _lib.status_string(-1)
+    assert "unknown" in _lib.status_string(-99)
+    assert b"gfx950" in _lib.load().vsa_version()
+
+
+def test_entry_points_reject_bad_arguments_without_a_gpu():
+    lib = _lib.load()
+    # NULL pointers and impossible sizes are rejected before any launch.
+    assert lib.vsa_pool_qkv(None, None, None, None, None, None, None, None,
+                            1, 64, 64, 128, 64, 0, None) == -1
+    assert lib.vsa_topk(None, None, 1, 4, 2, None) == -1
+    p = _lib.ptr(torch.zeros(1))
+    assert lib.vsa_topk(p, p, 1, 4, 5, None) == -2          # topk > Kb
+    assert lib.vsa_csr_build(p, p, p, p, 1, 4, 0, 2, None) == -2
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0,
+                              1, 100, 128, 128, 64, 1, 0.1, 0, None) == -2   # 100 % 64
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0,
+                              1, 96, 96, 128, 96, 1, 0.1, 0, None) == -4     # be 96: no kernel
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0,
+                              1, 64, 64, 128, 64, 1, 0.1, 2, None) == -3     # fp32 on MFMA path
+
+
+def _full(nb, be):
+    return torch.full((nb,), be, dtype=torch.long)
+
+
+def test_validation_texts_match_reference():
+    q = torch.randn(1, 1, 10, 8)
+    with pytest.raises(ValueError, match="divisible"):
+        M.mi355x_vsa(q, q, q, _full(2, 4), _full(2, 4), topk=1, block_size=(1, 1, 4))
+    q = torch.randn(1, 1, 12, 8)
+    with pytest.raises(ValueError, match="variable_block_sizes"):
+        M.mi355x_vsa(q, q, q, _full(2, 4), _full(2, 4), topk=1, block_size=(1, 1, 4))
+    with pytest.raises(ValueError, match="topk"):
+        M.mi355x_vsa(q, q, q, _full(3, 4), _full(3, 4), topk=4, block_size=(1, 1, 4))
+
+
+def test_cpu_tensors_are_rejected_not_computed_elsewhere():
+    q = torch.randn(1, 1, 128, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        M.mi355x_vsa(q, q, q, _full(2, 64), _full(2, 64), topk=1, block_size=(1, 1, 64))
+    sel = torch.zeros(1, 1, 2, 1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        M.mi355x_sparse_attention(q, q, q, sel, _full(2, 64), block_size=(1, 1, 64))
+
+
+def test_block_volume_and_gate_shape_helpers():
+    assert M.as_block_elements((4, 8, 8)) == 256
+    assert M.as_block_elements(4) == 64
+    q = torch.randn(1, 2, 16, 8)
+    assert M._prepare_gate(torch.ones(1, 2, 16, 1), q).shape == (1, 2, 16, 1)
+    with pytest.raises(ValueError, match="compress_attn_weight"):
+        M._prepare_gate(torch.ones(1, 2, 16, 4), q)
