@@ -26,13 +26,8 @@ struct DqCfg {
   static constexpr int NW = QT / 32;
   static constexpr int NT = NW * 64;
   static constexpr int KC = 64;
-  static constexpr int KP = D + 8;   // natural row pitch
-  static constexpr int TP = KC + 8;  // transposed row pitch
-  static constexpr int KS = KC * KP;
-  static constexpr int KT = D * TP;
-  static constexpr int STAGE = 2 * KS + KT;  // K, V natural + K transposed
-  static constexpr int UNITS = (KC / 4) * (D / 8);  // 4 keys x 8 dims
-  static constexpr int U_PER_T = (UNITS + NT - 1) / NT;
+  static constexpr int TILE = KC * D;            // one K (or V) chunk, swizzled row-major
+  static constexpr int STAGE = 2 * TILE;
 };
 
 template <int BE>
@@ -63,10 +58,7 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   using C = DqCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
-  __shared__ __attribute__((aligned(16))) T smem[C::STAGE];
-  T* Ks = smem;
-  T* Vs = Ks + C::KS;
-  T* Kt = Vs + C::KS;
+  __shared__ __attribute__((aligned(16))) T smem[2 * C::STAGE];
 
   const int tile = xcd_tile(blockIdx.x, num_tiles);
   if (tile >= num_tiles) return;
@@ -97,42 +89,11 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   const T* kbase = k + (int64_t)b * skv * D;
   const T* vbase = v + (int64_t)b * skv * D;
 
-  u32x4 kreg[C::U_PER_T][4], vreg[C::U_PER_T][4];
-  auto gload = [&](int kvb, int ch) {
+  auto dma = [&](int kvb, int ch, int stg) {
     const int64_t off = ((int64_t)kvb * BE + ch * C::KC) * D;
-#pragma unroll
-    for (int i = 0; i < C::U_PER_T; ++i) {
-      const int u = tid + i * C::NT;
-      if (C::UNITS % C::NT == 0 || u < C::UNITS) {
-        const int kg = u & 15, dg = u >> 4;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int64_t o = off + (kg * 4 + rr) * D + dg * 8;
-          kreg[i][rr] = *reinterpret_cast<const u32x4*>(kbase + o);
-          vreg[i][rr] = *reinterpret_cast<const u32x4*>(vbase + o);
-        }
-      }
-    }
-  };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < C::U_PER_T; ++i) {
-      const int u = tid + i * C::NT;
-      if (C::UNITS % C::NT == 0 || u < C::UNITS) {
-        const int kg = u & 15, dg = u >> 4;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          *reinterpret_cast<u32x4*>(Ks + (kg * 4 + rr) * C::KP + dg * 8) = kreg[i][rr];
-          *reinterpret_cast<u32x4*>(Vs + (kg * 4 + rr) * C::KP + dg * 8) = vreg[i][rr];
-        }
-        u32x2 cols[8];
-        transpose4x8_b16(kreg[i], cols);
-        const int pos = (kg >> 2) * 16 + group4_pos(kg & 3) * 4;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<u32x2*>(Kt + (dg * 8 + j) * C::TP + pos) = cols[j];
-      }
-    }
+    T* Ks = smem + stg * C::STAGE;
+    dma_tile<T, D, C::KC, C::NT>(Ks, kbase + off);
+    dma_tile<T, D, C::KC, C::NT>(Ks + C::TILE, vbase + off);
   };
 
   f32x16 dqacc[D / 32];
@@ -141,15 +102,17 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
 
   int s = 0, ch = 0, kv = 0, nvb = 0;
   bool have = next_valid_chunk_b<BE>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
-  if (have) gload(kv, ch);
+  if (have) dma(kv, ch, 0);
+  dma_wait();
+  __syncthreads();
+  int stage = 0;
   while (have) {
     const int nv = min(nvb - ch * 64, 64);
-    __syncthreads();  // previous chunk fully consumed
-    lstore();
-    __syncthreads();
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
     const bool have2 = next_valid_chunk_b<BE>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
-    if (have2) gload(kv2, ch2);
+    if (have2) dma(kv2, ch2, stage ^ 1);
+    const T* Ks = smem + stage * C::STAGE;
+    const T* Vs = Ks + C::TILE;
 
     f32x16 sacc[2] = {f32x16{}, f32x16{}};
     f32x16 pacc[2] = {f32x16{}, f32x16{}};
@@ -157,40 +120,32 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
       for (int smt = 0; smt < 2; ++smt) {
-        const int row = (smt * 32 + r) * C::KP + ks * 16 + h * 8;
-        const V8 ak = as_vec8<T>(*reinterpret_cast<const u32x4*>(Ks + row));
-        const V8 av = as_vec8<T>(*reinterpret_cast<const u32x4*>(Vs + row));
-        sacc[smt] = E::mfma32(ak, qf[ks], sacc[smt]);
-        pacc[smt] = E::mfma32(av, df[ks], pacc[smt]);
+        sacc[smt] = E::mfma32(row_a8<T, D>(Ks, smt * 32 + r, ks, h), qf[ks], sacc[smt]);
+        pacc[smt] = E::mfma32(row_a8<T, D>(Vs, smt * 32 + r, ks, h), df[ks], pacc[smt]);
       }
     }
-    float dsv[2][16];
-#pragma unroll
-    for (int smt = 0; smt < 2; ++smt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = exp2f(fmaf(sacc[smt][i], c2, -my_lse));
-        dsv[smt][i] = p * (pacc[smt][i] - my_delta);
-      }
-    if (nv < 64) {
-#pragma unroll
-      for (int smt = 0; smt < 2; ++smt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (key >= nv) dsv[smt][i] = 0.f;
-        }
-    }
+    // dS^T = P^T (dP^T - delta), consumed 8 keys at a time as the B operand
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const V8 bop = pack8<T>(&dsv[kk >> 1][8 * (kk & 1)]);
+      float dsv[8];
 #pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt) {
-        const V8 a = as_vec8<T>(
-            *reinterpret_cast<const u32x4*>(Kt + (mt * 32 + r) * C::TP + kk * 16 + h * 8));
-        dqacc[mt] = E::mfma32(a, bop, dqacc[mt]);
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * (kk & 1) + e;
+        const float p = fast_exp2(fmaf(sacc[kk >> 1][i], c2, -my_lse));
+        dsv[e] = p * (pacc[kk >> 1][i] - my_delta);
+        if (nv < 64) {
+          const int key = (kk >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (key >= nv) dsv[e] = 0.f;
+        }
       }
+      const V8 bop = pack8<T>(dsv);
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt)
+        dqacc[mt] = E::mfma32(tr_a8<T, D>(Ks, mt * 32, 16 * kk, 16 * kk + 8), bop, dqacc[mt]);
     }
+    dma_wait();
+    __syncthreads();
+    stage ^= 1;
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
   }
 
@@ -236,19 +191,14 @@ struct DkvCfg {
   static constexpr int KT = BE >= 128 ? 128 : BE;  // keys per workgroup
   static constexpr int NW = KT / 32;
   static constexpr int NT = NW * 64;
-  static constexpr int QS = 32;      // queries per LDS stage
-  static constexpr int NP = D + 8;   // natural row pitch
-  static constexpr int TP = QS + 8;  // transposed row pitch
-  static constexpr int NS = QS * NP;
-  static constexpr int TS = D * TP;
-  static constexpr int STAGE = 2 * NS + 2 * TS;  // Q, dO natural + transposed
-  static constexpr int UNITS = 2 * (QS / 4) * (D / 8);  // both tensors
-  static constexpr int U_PER_T = (UNITS + NT - 1) / NT;
-  static constexpr int SUBS = BE / QS;  // sub-tiles per query block
+  static constexpr int QS = 32;                    // queries per LDS stage
+  static constexpr int TILE = QS * D;              // one Q (or dO) sub-tile, swizzled
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int SUBS = BE / QS;             // sub-tiles per query block
 };
 
 template <typename T, int D, int BE>
-__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) void sparse_dkdv_kernel(
+__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void sparse_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
@@ -297,51 +247,18 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) void sparse_dkdv_kernel(
   const float* lbase = lse + (int64_t)b * sq;
   const float* ebase = delta + (int64_t)b * sq;
 
-  u32x4 reg[C::U_PER_T][4];
-  float stat_reg = 0.f;
-  auto gload = [&](int item) {
+  // Q / dO sub-tile -> two swizzled LDS tiles; lse / delta (32 + 32 floats)
+  // -> sstat[stg] through one dword-wide direct load by wave 0.
+  auto dma = [&](int item, int stg) {
     const int qblock = seg[item / C::SUBS];
     const int qrow0 = qblock * BE + (item % C::SUBS) * C::QS;
-#pragma unroll
-    for (int i = 0; i < C::U_PER_T; ++i) {
-      const int u = tid + i * C::NT;
-      if (C::UNITS % C::NT == 0 || u < C::UNITS) {
-        const int tsel = u / (C::UNITS / 2);  // 0: q, 1: dout
-        const int uu = u % (C::UNITS / 2);
-        const int qg = uu & 7, dg = uu >> 3;
-        const T* src = (tsel ? dbase : qbase) + (int64_t)(qrow0 + qg * 4) * D + dg * 8;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) reg[i][rr] = *reinterpret_cast<const u32x4*>(src + rr * D);
-      }
+    T* base = smem + stg * C::STAGE;
+    dma_tile<T, D, C::QS, C::NT>(base, qbase + (int64_t)qrow0 * D);
+    dma_tile<T, D, C::QS, C::NT>(base + C::TILE, dbase + (int64_t)qrow0 * D);
+    if (tid < 64) {
+      const float* src = tid < C::QS ? lbase + qrow0 + tid : ebase + qrow0 + (tid - C::QS);
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)&sstat[stg][0][0], 4, 0, 0);
     }
-    if (tid < 2 * C::QS) {
-      const int qq = tid % C::QS;
-      stat_reg = tid < C::QS ? lbase[qrow0 + qq] : ebase[qrow0 + qq];
-    }
-  };
-  auto lstore = [&](int stage) {
-    T* base = smem + stage * C::STAGE;
-#pragma unroll
-    for (int i = 0; i < C::U_PER_T; ++i) {
-      const int u = tid + i * C::NT;
-      if (C::UNITS % C::NT == 0 || u < C::UNITS) {
-        const int tsel = u / (C::UNITS / 2);
-        const int uu = u % (C::UNITS / 2);
-        const int qg = uu & 7, dg = uu >> 3;
-        T* nat = base + tsel * C::NS;
-        T* tr = base + 2 * C::NS + tsel * C::TS;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          *reinterpret_cast<u32x4*>(nat + (qg * 4 + rr) * C::NP + dg * 8) = reg[i][rr];
-        u32x2 cols[8];
-        transpose4x8_b16(reg[i], cols);
-        const int pos = (qg >> 2) * 16 + group4_pos(qg & 3) * 4;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<u32x2*>(tr + (dg * 8 + j) * C::TP + pos) = cols[j];
-      }
-    }
-    if (tid < 2 * C::QS) sstat[stage][tid / C::QS][tid % C::QS] = stat_reg;
   };
 
   f32x16 dkacc[D / 32], dvacc[D / 32];
@@ -351,60 +268,49 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) void sparse_dkdv_kernel(
     dvacc[mt] = f32x16{};
   }
 
-  if (items > 0) {
-    gload(0);
-    lstore(0);
-  }
+  if (items > 0) dma(0, 0);
+  dma_wait();
   __syncthreads();
   int stage = 0;
   for (int it = 0; it < items; ++it) {
     const bool more = it + 1 < items;
-    if (more) gload(it + 1);
-    const T* base = smem + stage * C::STAGE;
-    const T* Qs = base;
-    const T* Ds = base + C::NS;
-    const T* Qt = base + 2 * C::NS;
-    const T* Dt = Qt + C::TS;
+    if (more) dma(it + 1, stage ^ 1);
+    const T* Qs = smem + stage * C::STAGE;
+    const T* Ds = Qs + C::TILE;
 
     // S = Q K^T and dP = dO V^T: 32 queries x 32 keys
     f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      const int row = r * C::NP + ks * 16 + h * 8;
-      const V8 aq = as_vec8<T>(*reinterpret_cast<const u32x4*>(Qs + row));
-      const V8 ad = as_vec8<T>(*reinterpret_cast<const u32x4*>(Ds + row));
-      sacc = E::mfma32(aq, kf[ks], sacc);
-      pacc = E::mfma32(ad, vf[ks], pacc);
+      sacc = E::mfma32(row_a8<T, D>(Qs, r, ks, h), kf[ks], sacc);
+      pacc = E::mfma32(row_a8<T, D>(Ds, r, ks, h), vf[ks], pacc);
     }
-    // rows of this lane: queries 8g + 4h + e
-    float pv[16], dsv[16];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 l4 = *reinterpret_cast<const f32x4*>(&sstat[stage][0][8 * g + 4 * h]);
-      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sstat[stage][1][8 * g + 4 * h]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 4 * g + e;
-        const float p = key_valid ? exp2f(fmaf(sacc[i], c2, -l4[e])) : 0.f;
-        pv[i] = p;
-        dsv[i] = p * (pacc[i] - d4[e]);
-      }
-    }
-    // dV^T += dO^T P ; dK^T += Q^T dS   (reduce over the 32 queries)
+    // rows of this lane: queries 8g + 4h + e; consumed 8 queries (g = 2j, 2j+1)
+    // at a time: dV^T += dO^T P ; dK^T += Q^T dS
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const V8 bp = pack8<T>(&pv[8 * j]);
-      const V8 bs = pack8<T>(&dsv[8 * j]);
+      float pv[8], dsv[8];
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const int g = 2 * j + gg;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&sstat[stage][0][8 * g + 4 * h]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sstat[stage][1][8 * g + 4 * h]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p = key_valid ? fast_exp2(fmaf(sacc[4 * g + e], c2, -l4[e])) : 0.f;
+          pv[4 * gg + e] = p;
+          dsv[4 * gg + e] = p * (pacc[4 * g + e] - d4[e]);
+        }
+      }
+      const V8 bp = pack8<T>(pv);
+      const V8 bs = pack8<T>(dsv);
 #pragma unroll
       for (int mt = 0; mt < D / 32; ++mt) {
-        const int trow = (mt * 32 + r) * C::TP + j * 16 + h * 8;
-        const V8 ad = as_vec8<T>(*reinterpret_cast<const u32x4*>(Dt + trow));
-        const V8 aq = as_vec8<T>(*reinterpret_cast<const u32x4*>(Qt + trow));
-        dvacc[mt] = E::mfma32(ad, bp, dvacc[mt]);
-        dkacc[mt] = E::mfma32(aq, bs, dkacc[mt]);
+        dvacc[mt] = E::mfma32(tr_a8<T, D>(Ds, mt * 32, 16 * j, 16 * j + 8), bp, dvacc[mt]);
+        dkacc[mt] = E::mfma32(tr_a8<T, D>(Qs, mt * 32, 16 * j, 16 * j + 8), bs, dkacc[mt]);
       }
     }
-    if (more) lstore(stage ^ 1);
+    dma_wait();
     __syncthreads();
     stage ^= 1;
   }

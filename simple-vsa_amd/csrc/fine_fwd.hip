@@ -6,16 +6,20 @@
 // Work decomposition: one workgroup owns QT query rows of one (b, h) (QT = 128
 // for block volume >= 128, else the block), one wave owns 32 of them.  The
 // workgroup walks the selected KV blocks of its query block in 64-key chunks;
-// every chunk is staged in LDS once (K row-major, V transposed) and shared by
-// all waves; the next chunk's global loads are in flight while the current
-// chunk is multiplied (double-buffered LDS, one barrier per chunk).
+// every chunk is copied once into LDS (direct global->LDS loads) as two
+// swizzled row-major tiles (K and V) shared by all waves; the next chunk's
+// copy is in flight while the current chunk is multiplied (double-buffered
+// LDS, one barrier per chunk).
 //
 // Per wave and chunk:
 //   S^T (64 x 32)  = K (64 x D) . Q^T (D x 32)           A = K from LDS, B = Q in VGPRs
 //   online softmax per query (each lane owns one query: column r of S^T)
-//   O^T (D x 32)  += V^T (D x 64) . P^T (64 x 32)        A = V^T from LDS, B = P in VGPRs
+//   O^T (D x 32)  += V^T (D x 64) . P^T (64 x 32)        A = V^T by transpose reads, B = P
 // Holding S and O transposed keeps the softmax statistics and the O rescale
-// lane-local; only the row max crosses the two lane halves.
+// lane-local; only the row max crosses the two lane halves.  The running max
+// is only moved when a chunk exceeds it by more than 2^kRescaleSlack (the
+// exponentials stay <= 2^8, exact in fp32 and within bf16 range), so the O
+// rescale runs on a few chunks instead of most.
 #include "vsa_device.h"
 #include "vsa_launch.h"
 
@@ -27,17 +31,11 @@ struct FwdCfg {
   static constexpr int NW = QT / 32;               // waves per workgroup
   static constexpr int NT = NW * 64;
   static constexpr int KC = 64;                    // keys per chunk
-  static constexpr int KP = D + 8;                 // K row pitch (elements)
-  static constexpr int VP = KC + 8;                // V^T row pitch (elements)
-  static constexpr int KS = KC * KP;
-  static constexpr int VS = D * VP;
-  static constexpr int STAGE = KS + VS;
-  static constexpr int K_PIECES = KC * D / 8;      // 16-byte pieces of a K chunk
-  static constexpr int K_PER_T = (K_PIECES + NT - 1) / NT;
-  static constexpr int V_UNITS = (KC / 4) * (D / 8);  // 4 keys x 8 dims per unit
-  static constexpr int V_PER_T = (V_UNITS + NT - 1) / NT;
-  static constexpr int NCHUNK = BE / KC;
+  static constexpr int TILE = KC * D;              // elements of one K (or V) chunk
+  static constexpr int STAGE = 2 * TILE;           // K and V
 };
+
+constexpr float kRescaleSlack = 8.0f;  // log2 units
 
 // Advance (slot, chunk) to the next chunk that holds at least one valid key.
 template <int BE>
@@ -93,53 +91,11 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   const T* kbase = k + (int64_t)b * skv * D;
   const T* vbase = v + (int64_t)b * skv * D;
 
-  u32x4 kreg[C::K_PER_T];
-  u32x4 vreg[C::V_PER_T][4];
-  auto gload = [&](int kvb, int ch) {
+  auto dma = [&](int kvb, int ch, int stg) {
     const int64_t off = ((int64_t)kvb * BE + ch * C::KC) * D;
-    const T* kp = kbase + off;
-    const T* vp = vbase + off;
-#pragma unroll
-    for (int i = 0; i < C::K_PER_T; ++i) {
-      const int p = tid + i * C::NT;
-      if (C::K_PIECES % C::NT == 0 || p < C::K_PIECES)
-        kreg[i] = *reinterpret_cast<const u32x4*>(kp + p * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < C::V_PER_T; ++i) {
-      const int u = tid + i * C::NT;
-      if (C::V_UNITS % C::NT == 0 || u < C::V_UNITS) {
-        const int kg = u & 15, dg = u >> 4;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          vreg[i][rr] = *reinterpret_cast<const u32x4*>(vp + (kg * 4 + rr) * D + dg * 8);
-      }
-    }
-  };
-  auto lstore = [&](int stage) {
-    T* Ks = smem + stage * C::STAGE;
-    T* Vt = Ks + C::KS;
-#pragma unroll
-    for (int i = 0; i < C::K_PER_T; ++i) {
-      const int p = tid + i * C::NT;
-      if (C::K_PIECES % C::NT == 0 || p < C::K_PIECES) {
-        const int key = p / (D / 8), dc = p % (D / 8);
-        *reinterpret_cast<u32x4*>(Ks + key * C::KP + dc * 8) = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < C::V_PER_T; ++i) {
-      const int u = tid + i * C::NT;
-      if (C::V_UNITS % C::NT == 0 || u < C::V_UNITS) {
-        const int kg = u & 15, dg = u >> 4;
-        u32x2 cols[8];
-        transpose4x8_b16(vreg[i], cols);
-        const int pos = (kg >> 2) * 16 + group4_pos(kg & 3) * 4;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *reinterpret_cast<u32x2*>(Vt + (dg * 8 + j) * C::VP + pos) = cols[j];
-      }
-    }
+    T* Ks = smem + stg * C::STAGE;
+    dma_tile<T, D, C::KC, C::NT>(Ks, kbase + off);
+    dma_tile<T, D, C::KC, C::NT>(Ks + C::TILE, vbase + off);
   };
 
   float m = -INFINITY;  // running max in log2 units (scaled)
@@ -150,33 +106,27 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 
   int s = 0, ch = 0, kv = 0, nvb = 0;
   bool have = next_valid_chunk<BE>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
-  if (have) {
-    gload(kv, ch);
-    lstore(0);
-  }
+  if (have) dma(kv, ch, 0);
+  dma_wait();
   __syncthreads();
   int stage = 0;
   while (have) {
     const int nv = min(nvb - ch * 64, 64);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
     const bool have2 = next_valid_chunk<BE>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
-    if (have2) gload(kv2, ch2);
+    if (have2) dma(kv2, ch2, stage ^ 1);  // lands while this chunk is multiplied
 
     const T* Ks = smem + stage * C::STAGE;
-    const T* Vt = Ks + C::KS;
+    const T* Vs = Ks + C::TILE;
     // ---- S^T = K Q^T -------------------------------------------------------
     f32x16 sacc[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
-      for (int smt = 0; smt < 2; ++smt) {
-        const V8 a = as_vec8<T>(
-            *reinterpret_cast<const u32x4*>(Ks + (smt * 32 + r) * C::KP + ks * 16 + h * 8));
-        sacc[smt] = E::mfma32(a, qf[ks], sacc[smt]);
-      }
+      for (int smt = 0; smt < 2; ++smt)
+        sacc[smt] = E::mfma32(row_a8<T, D>(Ks, smt * 32 + r, ks, h), qf[ks], sacc[smt]);
     }
-    // ---- online softmax (base 2) ------------------------------------------
-    float smax = -INFINITY;
+    // ---- online softmax (base 2, lazily rescaled) ---------------------------
     if (nv < 64) {
 #pragma unroll
       for (int smt = 0; smt < 2; ++smt)
@@ -186,14 +136,15 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
           if (key >= nv) sacc[smt][i] = -INFINITY;
         }
     }
+    float smax = sacc[0][0];
 #pragma unroll
     for (int smt = 0; smt < 2; ++smt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) smax = fmaxf(smax, sacc[smt][i]);
-    smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
-    const float mnew = fmaxf(m, smax * c2);
-    if (__any(mnew > m)) {  // exact: alpha == 1 where the max did not move
-      const float alpha = exp2f(m - mnew);
+    smax = fmaxf(smax, __shfl_xor(smax, 32, 64)) * c2;
+    if (__any(smax > m + kRescaleSlack)) {
+      const float mnew = fmaxf(m, smax);
+      const float alpha = fast_exp2(m - mnew);
       lsum *= alpha;
 #pragma unroll
       for (int mt = 0; mt < D / 32; ++mt) oacc[mt] *= alpha;
@@ -204,9 +155,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 #pragma unroll
     for (int smt = 0; smt < 2; ++smt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        p[smt][i] = exp2f(fmaf(sacc[smt][i], c2, negm));
-      }
+      for (int i = 0; i < 16; ++i) p[smt][i] = fast_exp2(fmaf(sacc[smt][i], c2, negm));
     if (nv < 64) {
 #pragma unroll
       for (int smt = 0; smt < 2; ++smt)
@@ -220,19 +169,16 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     for (int smt = 0; smt < 2; ++smt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) lsum += p[smt][i];
-    // ---- O^T += V^T P^T -------------------------------------------------------
+    // ---- O^T += V^T P^T ------------------------------------------------------
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const V8 bop = pack8<T>(&p[kk >> 1][8 * (kk & 1)]);
 #pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt) {
-        const V8 a = as_vec8<T>(
-            *reinterpret_cast<const u32x4*>(Vt + (mt * 32 + r) * C::VP + kk * 16 + h * 8));
-        oacc[mt] = E::mfma32(a, bop, oacc[mt]);
-      }
+      for (int mt = 0; mt < D / 32; ++mt)
+        oacc[mt] = E::mfma32(tr_a8<T, D>(Vs, mt * 32, 16 * kk, 16 * kk + 8), bop, oacc[mt]);
     }
 
-    if (have2) lstore(stage ^ 1);
+    dma_wait();
     __syncthreads();
     stage ^= 1;
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;

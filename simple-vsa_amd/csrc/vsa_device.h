@@ -83,6 +83,130 @@ __device__ __forceinline__ typename Elem<T>::vec8 as_vec8(u32x4 x) {
 }
 
 // ---------------------------------------------------------------------------
+// Swizzled row-major LDS tiles.
+//
+// A tile X[s][d] (s = sequence row, d = head dim, D elements per row) is kept
+// unpadded; its 16-byte chunk c of row r lives at chunk position c ^ f(r).
+// The XOR keeps three access patterns free of bank conflicts on the 64-bank
+// gfx950 LDS:
+//   * MFMA row reads: 16 lanes read chunk c of 16 consecutive rows;
+//   * stores: 16 lanes write the 16 chunks of one row (D = 128) or two rows
+//     (D = 64);
+//   * transpose reads (ds_read_b64_tr_b16): 32 lanes read 8 bytes each from 4
+//     consecutive rows x 64 contiguous bytes.
+// For D = 64 two rows form one 256-byte super-row and the XOR acts on it.
+// Returns the element offset of the first element of the chunk.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ int swz(int r, int c);
+
+template <>
+__device__ __forceinline__ int swz<128>(int r, int c) {
+  return r * 128 + ((c ^ (((r & 3) << 2) | ((r >> 2) & 3))) << 3);
+}
+
+template <>
+__device__ __forceinline__ int swz<64>(int r, int c) {
+  const int R = r >> 1, C = ((r & 1) << 3) | c;
+  return R * 128 + ((C ^ (((R & 1) << 2) | ((R >> 1) & 3))) << 3);
+}
+
+// Element offset of X[r][d] for d a multiple of 4 (8-byte aligned pieces).
+template <int D>
+__device__ __forceinline__ int swz_elem(int r, int d) {
+  return swz<D>(r, d >> 3) + (d & 7);
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// A operand (32 x 16, rows m = d0 .. d0+31, k = 8 sequence rows) of a
+// 32x32x16 MFMA that reduces over the sequence, read from a swizzled
+// row-major tile X[s][d] with two ds_read_b64_tr_b16.  Lane (r, h) receives
+// X[sA(h) + 0..3][d0 + r] followed by X[sB(h) + 0..3][d0 + r], where
+// sA(h) = sa + 4h and sB(h) = sb + 4h.
+//
+// ds_read_b64_tr_b16 (gfx950): inside each 16-lane group, lane i receives
+// element i%4 of the 8-byte pieces addressed by lanes i/4, 4+i/4, 8+i/4 and
+// 12+i/4 of that group.  Lane j = 4e + g of group (q, h) therefore addresses
+// row s + e, dims d0 + 16q + 4g .. +3.
+template <typename T, int D>
+__device__ __forceinline__ typename Elem<T>::vec8 tr_a8(const T* X, int d0, int sa, int sb) {
+  const int lane = threadIdx.x & 63;
+  const int grp = lane >> 4, j = lane & 15;
+  const int q = grp & 1, h = grp >> 1;
+  const int d = d0 + 16 * q + 4 * (j & 3);
+  const int e = j >> 2;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(X + swz_elem<D>(sa + 4 * h + e, d)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(X + swz_elem<D>(sb + 4 * h + e, d)));
+  u32x4 r;
+  r[0] = __builtin_bit_cast(u32x2, lo)[0];
+  r[1] = __builtin_bit_cast(u32x2, lo)[1];
+  r[2] = __builtin_bit_cast(u32x2, hi)[0];
+  r[3] = __builtin_bit_cast(u32x2, hi)[1];
+  return as_vec8<T>(r);
+}
+
+// Row read for an MFMA operand: lane (r, h) gets X[row][16*ks + 8h .. +7].
+template <typename T, int D>
+__device__ __forceinline__ typename Elem<T>::vec8 row_a8(const T* X, int row, int ks, int h) {
+  return as_vec8<T>(*reinterpret_cast<const u32x4*>(X + swz<D>(row, 2 * ks + h)));
+}
+
+// ---------------------------------------------------------------------------
+// Direct global -> LDS copies (global_load_lds_dwordx4: lane i of a wave
+// writes 16 bytes at LDS base + 16*i).  Each lane fetches the global chunk
+// that the swizzle places at its LDS slot, so a row-major global tile lands
+// in the swizzled layout without passing through VGPRs.  Completion is
+// tracked by vmcnt: call dma_wait() before the barrier that publishes it.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int D>
+__device__ __forceinline__ int unswz_row_chunk(int P, int& c);  // P: LDS chunk index
+
+template <>
+__device__ __forceinline__ int unswz_row_chunk<128>(int P, int& c) {
+  const int row = P >> 4;
+  c = (P & 15) ^ (((row & 3) << 2) | ((row >> 2) & 3));
+  return row;
+}
+
+template <>
+__device__ __forceinline__ int unswz_row_chunk<64>(int P, int& c) {
+  const int R = P >> 4;
+  const int C = (P & 15) ^ (((R & 1) << 2) | ((R >> 1) & 3));
+  c = C & 7;
+  return 2 * R + (C >> 3);
+}
+
+// Copy a NROWS x D row-major global tile into the swizzled LDS tile `dst`.
+// All NT threads of the workgroup call it.
+template <typename T, int D, int NROWS, int NT>
+__device__ __forceinline__ void dma_tile(T* dst, const T* __restrict__ src) {
+  constexpr int CHUNKS = NROWS * D / 8;
+  static_assert(CHUNKS % NT == 0, "tile must split evenly over the workgroup");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < CHUNKS / NT; ++i) {
+    const int blk = i * (NT / 64) + wave;  // 1 KiB block written by this wave
+    int c;
+    const int row = unswz_row_chunk<D>(blk * 64 + lane, c);
+    __builtin_amdgcn_global_load_lds((const void*)(src + row * D + c * 8),
+                                     (lds_void*)(dst + blk * (1024 / (int)sizeof(T))), 16, 0, 0);
+  }
+}
+
+// Wait for this wave's outstanding vector-memory loads (vmcnt = 0).
+__device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// exp2 on the transcendental unit without the libm range fix-ups
+// (results below 2^-126 flush to zero, which softmax weights tolerate).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
 // Transposed-tile bookkeeping.
 //   seq_pos16(s): LDS position (inside a 16-group) of sequence index s, so that
 //   lane half h reading positions 8h .. 8h+7 receives sequence indices
