@@ -49,9 +49,10 @@ def _events_time(fn, iters):
     return start.elapsed_time(end) / iters
 
 
-def cpu_baseline(heads: int = 1):
+def cpu_baseline(heads: int = 8):
     """The CPU oracle (a restatement of torch_vsa) fwd+bwd on `heads` heads of
-    the workload; returns (TFLOP/s, seconds, threads)."""
+    the workload, one head at a time (heads are independent; one head's
+    fp32 intermediates are a few GB).  Returns (TFLOP/s, seconds, threads)."""
     import torch
     sys.path.insert(0, ROOT)
     from oracle import vsa_oracle as O
@@ -59,17 +60,20 @@ def cpu_baseline(heads: int = 1):
     B, S, D, topk = CFG["B"], CFG["S"], CFG["D"], CFG["topk"]
     be = math.prod(CFG["block"])
     g = torch.Generator().manual_seed(0)
-    shape = (B, heads, S, D)
-    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16).requires_grad_()
-                   for _ in range(4))
-    gate = torch.rand(shape, generator=g).to(torch.bfloat16).requires_grad_()
     vbs = torch.full((S // be,), be)
-    t0 = time.perf_counter()
-    out = O.torch_vsa(q, k, v, vbs, vbs, topk, CFG["block"], gate)
-    torch.autograd.grad(out, (q, k, v, gate), do.detach())
-    dt = time.perf_counter() - t0
+    total = 0.0
+    for _ in range(heads):
+        shape = (B, 1, S, D)
+        q, k, v = (torch.randn(shape, generator=g).to(torch.bfloat16).requires_grad_()
+                   for _ in range(3))
+        do = torch.randn(shape, generator=g).to(torch.bfloat16)
+        gate = torch.rand(shape, generator=g).to(torch.bfloat16).requires_grad_()
+        t0 = time.perf_counter()
+        out = O.torch_vsa(q, k, v, vbs, vbs, topk, CFG["block"], gate)
+        torch.autograd.grad(out, (q, k, v, gate), do)
+        total += time.perf_counter() - t0
     f = 3.5 * flops_fwd(B, heads, S, D, be, topk)
-    return f / dt / 1e12, dt, threads
+    return f / total / 1e12, total, threads
 
 
 def main():
@@ -79,6 +83,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--kernels-only", action="store_true", help="skip the CPU baseline and summary")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy a 1 GiB buffer 3 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--cpu-heads", type=int, default=8,
+                    help="heads of the workload timed on the CPU oracle (one at a time)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every MI355X box "
@@ -87,6 +95,16 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_probe:
+        src = torch.ones(1 << 29, device="cuda", dtype=torch.bfloat16)   # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * src.element_size()}))
+        return
+
     from vsa import mi355x as M
 
     dev = torch.device("cuda", 0)
@@ -173,13 +191,20 @@ def main():
     dom_t, dom_f = kt[dom]
     achieved = dom_f / (dom_t * 1e-3) / 1e12
 
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"{dom}_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
     F_total = 3.5 * F_fwd
     value = F_total / (ms_step * 1e-3) / 1e12
     cpu = None
     if not (args.no_cpu or args.kernels_only):
-        cv, cs, cth = cpu_baseline(heads=1)
+        cv, cs, cth = cpu_baseline(heads=args.cpu_heads)
         cpu = {"value": round(cv, 4), "unit": "TFLOP/s", "cores": cth, "kind": "port",
-               "sample": f"oracle torch_vsa fwd+bwd, 1 of {H} heads of the workload "
+               "sample": f"oracle torch_vsa fwd+bwd, {args.cpu_heads} of {H} heads of the "
+                         "workload, one head at a time "
                          f"(B=1,H=1,S={S},D={D},be={be},topk={topk}, bf16 inputs), "
                          f"{cs:.1f} s wall, throughput in effective TFLOP/s"}
     line = {
@@ -204,7 +229,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
