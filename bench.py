@@ -31,6 +31,19 @@ HBM_PEAK_GBS = 8000.0
 
 CFG = dict(B=1, H=40, S=40960, D=128, block=(4, 8, 8), topk=20)
 
+# The BASELINE.json configurations that run on the GPU (configs[1..4]); c3 is
+# the metric's workload and the default.
+WORKLOADS = {
+    "c2": dict(name="Small GPU (BASELINE configs[1])", B=1, H=12, S=16384, D=128,
+               block=(1, 1, 256), topk=8, gate="token", last_valid=200),
+    "c3": dict(name="Video-DiT mid shape (BASELINE configs[2])", B=1, H=40, S=40960, D=128,
+               block=(4, 8, 8), topk=20, gate="full"),
+    "c4": dict(name="Long video shape (BASELINE configs[3])", B=1, H=40, S=92160, D=128,
+               block=(1, 1, 256), topk=45, gate=None, every8th=192, amp=0.5),
+    "c5": dict(name="Route-skew explicit routing (BASELINE configs[4])", B=1, H=24, S=40960,
+               D=64, block=(1, 1, 64), topk=32, gate=None, zipf=1.2),
+}
+
 
 def flops_fwd(B, H, S, D, be, topk):
     return 4.0 * B * H * (S // be) * topk * be * be * D
@@ -76,6 +89,79 @@ def cpu_baseline(heads: int = 8):
     return f / total / 1e12, total, threads
 
 
+def _zipf_routes(h, qb, kb, tk, s, seed=5):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, kb + 1) ** s
+    p /= p.sum()
+    perm = rng.permutation(kb)
+    sel = np.stack([np.stack([perm[rng.choice(kb, tk, replace=False, p=p)] for _ in range(qb)])
+                    for _ in range(h)])
+    return sel[None].astype(np.int32)
+
+
+def run_workload(key, steps, warmup):
+    """Time fwd and fwd+bwd of one BASELINE workload; report ms, effective
+    TFLOP/s and the peak HBM the op allocates beyond its inputs."""
+    import torch
+    from vsa import mi355x as M
+    w = WORKLOADS[key]
+    dev = torch.device("cuda", 0)
+    B, H, S, D, topk = w["B"], w["H"], w["S"], w["D"], w["topk"]
+    be = math.prod(w["block"])
+    nb = S // be
+    amp = w.get("amp", 1.0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16) * amp
+               for _ in range(3))
+    do = torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    gate = None
+    if w["gate"] == "full":
+        gate = torch.rand(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    elif w["gate"] == "token":
+        gate = torch.rand(B, H, S, 1, generator=g, device=dev, dtype=torch.bfloat16)
+    vbs = torch.full((nb,), be, dtype=torch.int32)
+    if "last_valid" in w:
+        vbs[-1] = w["last_valid"]
+    if "every8th" in w:
+        vbs[7::8] = w["every8th"]
+    vbs = vbs.to(dev)
+    leaves = [t.requires_grad_() for t in (q, k, v)] + ([gate.requires_grad_()] if gate is not None else [])
+    if "zipf" in w:
+        sel = torch.from_numpy(_zipf_routes(H, nb, nb, topk, w["zipf"])).to(dev)
+        fwd = lambda: M.mi355x_sparse_attention(q, k, v, sel, vbs, block_size=w["block"])
+    else:
+        fwd = lambda: M.mi355x_vsa(q, k, v, vbs, vbs, topk, w["block"], gate)
+
+    def step():
+        torch.autograd.grad(fwd(), leaves, do)
+
+    def fwd_only():
+        with torch.no_grad():
+            fwd()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    fms = _events_time(fwd_only, max(5, steps // 2))
+    F = flops_fwd(B, H, S, D, be, topk)   # padded volume, selected pairs only
+    return {"workload": key, "name": w["name"], "ms_fwd_bwd": round(ms, 3), "ms_fwd": round(fms, 3),
+            "tflops_fwd_bwd": round(3.5 * F / (ms * 1e-3) / 1e12, 1),
+            "tflops_fwd": round(F / (fms * 1e-3) / 1e12, 1),
+            "pct_bf16_peak_fwd_bwd": round(100 * 3.5 * F / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 2),
+            "peak_hbm_gib_beyond_inputs": round(peak / 2 ** 30, 3), "steps": steps}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,6 +173,8 @@ def main():
                     help="only copy a 1 GiB buffer 3 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--cpu-heads", type=int, default=8,
                     help="heads of the workload timed on the CPU oracle (one at a time)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3",
+                    help="BASELINE configuration to run (c3 is the metric's workload)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every MI355X box "
@@ -106,6 +194,10 @@ def main():
         return
 
     from vsa import mi355x as M
+
+    if args.workload != "c3":
+        print(json.dumps(run_workload(args.workload, args.steps, args.warmup)), flush=True)
+        return
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)

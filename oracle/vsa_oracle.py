@@ -25,6 +25,10 @@ Extra hooks that the reference does not have, for parity testing only:
   documented rule on the GPU, while ``torch.topk`` leaves tie order open);
 * ``torch_vsa(..., head_chunk=h)`` evaluates the fine branch ``h`` heads at a
   time so large configurations fit in host memory (heads are independent).
+
+One deliberate precision difference from ``torch_impl.py``: the fine branch
+gathers from fp32 copies of k and v, so gradients of a key block shared by
+many query blocks accumulate in fp32 (see ``_fine_branch``).
 """
 
 from __future__ import annotations
@@ -237,8 +241,14 @@ def _fine_branch(q, k, v, selected, vbs, be, scale):
     b, h, sq, d = q.shape
     qb = sq // be
     tk = selected.shape[-1]
-    sel_k = _acc(_gather_blocks(k, selected, be))
-    sel_v = _acc(_gather_blocks(v, selected, be))
+    # Gather from fp32 copies: forward values are the same as gathering in T
+    # and then promoting (torch_impl.py:86-87), but the backward of the gather
+    # then accumulates the per-query-block gradients of a shared key block in
+    # fp32.  Gathering in T (as torch_impl.py does) makes autograd accumulate
+    # them in bf16, which is off by ~1e-2 relative L2 on hot key blocks with
+    # hundreds of in-edges; the reference's Triton kernels accumulate in fp32.
+    sel_k = _gather_blocks(_acc(k), selected, be)
+    sel_v = _gather_blocks(_acc(v), selected, be)
     valid_sel = valid_token_mask(vbs, be)[selected.long()]          # [B,H,Qb,tk,be]
     query = _acc(q.reshape(b, h, qb, be, d))
     keys = sel_k.reshape(b, h, qb, tk * be, d)

@@ -34,10 +34,12 @@ template <int BE>
 __device__ __forceinline__ bool next_valid_chunk_b(const int32_t* __restrict__ sel,
                                                    const int32_t* __restrict__ vbs, int topk,
                                                    int kb, int& s, int& c, int& kv, int& nvb) {
+  // Uniform indices keep these reads on the scalar path: a vector load here
+  // would need vmcnt(0) and so wait for every K/V copy still in flight.
   while (s < topk) {
-    kv = sel[s];
+    kv = __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(s)]);
     if (kv >= 0 && kv < kb) {
-      nvb = clamp_valid(vbs[kv], BE);
+      nvb = __builtin_amdgcn_readfirstlane(clamp_valid(vbs[kv], BE));
       if (c * 64 < nvb) return true;
     }
     ++s;
@@ -257,7 +259,7 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     dma_tile<T, D, C::QS, C::NT>(base + C::TILE, dbase + (int64_t)qrow0 * D);
     if (tid < 64) {
       const float* src = tid < C::QS ? lbase + qrow0 + tid : ebase + qrow0 + (tid - C::QS);
-      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)&sstat[stg][0][0], 4, 0, 0);
+      dma4(src, __builtin_amdgcn_readfirstlane(lds_addr(&sstat[stg][0][0])));
     }
   };
 

@@ -42,10 +42,12 @@ template <int BE>
 __device__ __forceinline__ bool next_valid_chunk(const int32_t* __restrict__ sel,
                                                  const int32_t* __restrict__ vbs, int topk,
                                                  int kb, int& s, int& c, int& kv, int& nvb) {
+  // Uniform indices keep these reads on the scalar path: a vector load here
+  // would need vmcnt(0) and so wait for every K/V copy still in flight.
   while (s < topk) {
-    kv = sel[s];
+    kv = __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(s)]);
     if (kv >= 0 && kv < kb) {
-      nvb = clamp_valid(vbs[kv], BE);
+      nvb = __builtin_amdgcn_readfirstlane(clamp_valid(vbs[kv], BE));
       if (c * 64 < nvb) return true;
     }
     ++s;

@@ -182,6 +182,27 @@ __device__ __forceinline__ int unswz_row_chunk<64>(int P, int& c) {
   return 2 * R + (C >> 3);
 }
 
+// One global_load_lds_dwordx4 for this wave: lane i copies 16 bytes from `g`
+// to LDS byte address lds + 16*i (`lds` wave-uniform, passed through M0).
+// Issued as inline asm on purpose: when the compiler sees an LDS DMA in
+// flight it puts vmcnt(0) in front of later LDS reads it cannot disambiguate
+// (the transpose reads), which would drain the prefetch.  Every consumer of
+// the copied tile waits on vmcnt explicitly (dma_wait) before its barrier.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory");
+}
+
+// Same with 4 bytes per lane (LDS byte address lds + 4*i).
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds)
+               : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // Copy a NROWS x D row-major global tile into the swizzled LDS tile `dst`.
 // All NT threads of the workgroup call it.
 template <typename T, int D, int NROWS, int NT>
@@ -194,13 +215,44 @@ __device__ __forceinline__ void dma_tile(T* dst, const T* __restrict__ src) {
     const int blk = i * (NT / 64) + wave;  // 1 KiB block written by this wave
     int c;
     const int row = unswz_row_chunk<D>(blk * 64 + lane, c);
-    __builtin_amdgcn_global_load_lds((const void*)(src + row * D + c * 8),
-                                     (lds_void*)(dst + blk * (1024 / (int)sizeof(T))), 16, 0, 0);
+    dma16(src + row * D + c * 8,
+          __builtin_amdgcn_readfirstlane(lds_addr(dst + blk * (1024 / (int)sizeof(T)))));
   }
 }
 
+// Wait until at most N of this wave's vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Wait for this wave's outstanding vector-memory loads (vmcnt = 0).
-__device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ __forceinline__ void dma_wait() { wait_vmcnt<0>(); }
+
+// Ring depth for a workgroup of `nw` waves whose LDS stage is `stage_bytes`:
+// keep enough workgroups per CU for 8 waves (2 per SIMD) and give each as many
+// stages (min_stages..4) as its share of the 160 KiB LDS holds.
+constexpr int ring_depth(int nw, int stage_bytes, int min_stages = 2) {
+  const int wg_per_cu = 8 / nw;
+  const int budget = (163840 / wg_per_cu) < 131072 ? (163840 / wg_per_cu) : 131072;
+  const int fit = budget / stage_bytes;
+  return fit > 4 ? 4 : (fit < min_stages ? min_stages : fit);
+}
+
+// Ring of NS LDS stages, each filled by PER direct loads per thread: wait
+// until the oldest in-flight stage has landed while `newer` younger stages
+// may stay in flight (newer <= NS - 2).  Vector-memory loads retire in order.
+template <int PER, int NS>
+__device__ __forceinline__ void wait_ring(int newer) {
+  static_assert(NS >= 2 && NS <= 4, "ring depth 2..4");
+  if (NS >= 4 && newer >= 2)
+    wait_vmcnt<(NS >= 4 ? 2 * PER : 0)>();
+  else if (NS >= 3 && newer >= 1)
+    wait_vmcnt<(NS >= 3 ? PER : 0)>();
+  else
+    wait_vmcnt<0>();
+}
 
 // exp2 on the transcendental unit without the libm range fix-ups
 // (results below 2^-126 flush to zero, which softmax weights tolerate).
