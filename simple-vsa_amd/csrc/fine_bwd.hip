@@ -12,6 +12,8 @@
 //   S^T  = K Q^T,  dP^T = V dO^T,  dS^T = P^T (dP^T - delta),  dQ^T += K^T dS^T
 // dK/dV, per wave (32 keys) and 32-query sub-tile of an in-edge query block:
 //   S = Q K^T,  dP = dO V^T,  dS = P (dP - delta),  dV^T += dO^T P,  dK^T += Q^T dS
+#include <type_traits>
+
 #include "vsa_device.h"
 #include "vsa_launch.h"
 
@@ -186,7 +188,17 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
 }
 
 // ===========================================================================
-// dK / dV
+// dK / dV: one workgroup per KV tile of KT keys (wave w owns keys 32w..32w+31,
+// K^T/V^T fragments in VGPRs), looping over the 32-query sub-tiles ("items")
+// of the tile's CSR in-edges.  Per item i the wave computes
+//   A(i): S = Q_i K^T, dP = dO_i V^T             (MFMA, rows of the LDS tiles)
+//   B(i): P = exp2(S c2 - lse), dS = P (dP - delta)          (VALU)
+//   C(i): dV^T += dO_i^T P, dK^T += Q_i^T dS      (MFMA, transposed LDS reads)
+// software-pipelined so that A(i+1) is issued between the VALU work of B(i)
+// (an MFMA only overlaps VALU work of its own wave on CDNA4).  One wave per
+// SIMD: the accumulators live in AGPRs, and latency is covered inside the
+// wave by an LDS read stream L operands deep and an NS-stage LDS ring of
+// items filled by direct global->LDS loads spread over each step.
 // ===========================================================================
 template <int D, int BE>
 struct DkvCfg {
@@ -195,12 +207,33 @@ struct DkvCfg {
   static constexpr int NT = NW * 64;
   static constexpr int QS = 32;                    // queries per LDS stage
   static constexpr int TILE = QS * D;              // one Q (or dO) sub-tile, swizzled
-  static constexpr int STAGE = 2 * TILE;
   static constexpr int SUBS = BE / QS;             // sub-tiles per query block
+  static constexpr int NS = 4;                     // LDS ring depth (loop unrolled by NS)
+  static constexpr int TP = TILE / 8 / NT;         // direct loads per thread per tile
+  static constexpr int PER = 2 * TP + 1;           // direct loads per thread per item
+  static constexpr int SEGMAX = 2048;              // CSR entries staged in LDS
+  static constexpr int NA = 2 * (D / 16);          // MFMAs of A (S and dP interleaved)
+  static constexpr int NC = 4 * (D / 32);          // MFMAs of C (dV and dK interleaved)
+  static constexpr int L = 12;                     // LDS operand lookahead
 };
 
+// Keep a lane-dependent value in a register: the compiler would otherwise
+// rematerialise the address arithmetic at every use inside the loop.
+template <typename X>
+__device__ __forceinline__ X opaque(X x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Direct global -> LDS copy with a scalar base and a 32-bit lane offset.
+__device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds)
+               : "memory");
+}
+
 template <typename T, int D, int BE>
-__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void sparse_dkdv_kernel(
+__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
@@ -211,8 +244,10 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   using C = DkvCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
-  __shared__ __attribute__((aligned(16))) T smem[2 * C::STAGE];
-  __shared__ __attribute__((aligned(16))) float sstat[2][2][C::QS];  // [stage][lse, delta][query]
+  constexpr int NS = C::NS, NA = C::NA, NC = C::NC, L = C::L, TP = C::TP;
+  __shared__ __attribute__((aligned(16))) T smem[NS][2 * C::TILE];
+  __shared__ __attribute__((aligned(16))) float sstat[NS][2][C::QS];  // [stage][lse, delta][query]
+  __shared__ int32_t sseg[C::SEGMAX];
 
   const int tile = xcd_tile(blockIdx.x, num_tiles);
   if (tile >= num_tiles) return;
@@ -244,22 +279,83 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   const int nedge = counts[meta];
   const int32_t* seg = inverse + (int64_t)b * qb * topk + offsets[meta];
   const int items = nedge * C::SUBS;
+  // Retire the fragment loads before the ring starts: the compiler's own vmcnt
+  // bookkeeping does not see the direct loads, and a wait it placed in the
+  // loop for these registers would also drain the in-flight stages.
+  dma_wait();
   const T* qbase = q + (int64_t)b * sq * D;
   const T* dbase = dout + (int64_t)b * sq * D;
   const float* lbase = lse + (int64_t)b * sq;
   const float* ebase = delta + (int64_t)b * sq;
 
-  // Q / dO sub-tile -> two swizzled LDS tiles; lse / delta (32 + 32 floats)
-  // -> sstat[stg] through one dword-wide direct load by wave 0.
-  auto dma = [&](int item, int stg) {
-    const int qblock = seg[item / C::SUBS];
-    const int qrow0 = qblock * BE + (item % C::SUBS) * C::QS;
-    T* base = smem + stg * C::STAGE;
-    dma_tile<T, D, C::QS, C::NT>(base, qbase + (int64_t)qrow0 * D);
-    dma_tile<T, D, C::QS, C::NT>(base + C::TILE, dbase + (int64_t)qrow0 * D);
-    if (tid < 64) {
-      const float* src = tid < C::QS ? lbase + qrow0 + tid : ebase + qrow0 + (tid - C::QS);
-      dma4(src, __builtin_amdgcn_readfirstlane(lds_addr(&sstat[stg][0][0])));
+  // ---- per-lane LDS / global offsets (bytes), fixed for the whole loop ----
+  uint32_t row_off[D / 16];  // A rows: lane (r, h), dims 16ks + 8h .. +7
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * 2));
+  uint32_t tr_off[D / 32][2];  // C operands: rows 8hi + 4h + e, dims 32mt + 16q + 4g
+  {
+    const int grp = lane >> 4, jl = lane & 15;
+    const int qq = grp & 1, hh = grp >> 1;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+        tr_off[mt][hi] = opaque((uint32_t)(
+            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3)) * 2));
+  }
+  const uint32_t st_off = opaque((uint32_t)(4 * h * 4));
+  uint32_t cp_goff[TP], cp_loff[TP];  // direct-load pieces: global offset, LDS block
+#pragma unroll
+  for (int i = 0; i < TP; ++i) {
+    const int blk = i * (C::NT / 64) + wave;
+    int c;
+    const int row = unswz_row_chunk<D>(blk * 64 + lane, c);
+    cp_goff[i] = opaque((uint32_t)((row * D + c * 8) * 2));
+    cp_loff[i] = (uint32_t)(blk * 1024);
+  }
+  const uint32_t smem_lds = lds_addr(&smem[0][0]);
+  const uint32_t sstat_lds = lds_addr(&sstat[0][0][0]);
+  const char* smem_c = reinterpret_cast<const char*>(&smem[0][0]);
+  const char* sstat_c = reinterpret_cast<const char*>(&sstat[0][0][0]);
+
+  // CSR segment staged in LDS, SEGMAX entries at a time (a scalar load per
+  // item would put scalar-memory latency in front of every copy, a vector
+  // load would need vmcnt(0) and drain the ring).  The refill runs where every
+  // wave has finished with the previous entries (all waves call qblock_of at
+  // the same program point, between two barriers).
+  int seg_lo = 0, seg_hi = 0;
+  auto qblock_of = [&](int item) {
+    const int e = item / C::SUBS;
+    if (e >= seg_hi) {
+      __syncthreads();
+      seg_lo = e;
+      seg_hi = e + C::SEGMAX;
+      for (int i = tid; i < C::SEGMAX && seg_lo + i < nedge; i += C::NT) sseg[i] = seg[seg_lo + i];
+      __syncthreads();
+    }
+    return __builtin_amdgcn_readfirstlane(sseg[e - seg_lo]);
+  };
+  struct Copy {
+    const char* qsrc;
+    const char* dsrc;
+    const float* ssrc;  // per lane: lse (lanes < 32) or delta
+  };
+  auto copy_of = [&](int item) {
+    Copy cp;
+    const int qrow0 = qblock_of(item) * BE + (item % C::SUBS) * C::QS;
+    cp.qsrc = reinterpret_cast<const char*>(qbase + (int64_t)qrow0 * D);
+    cp.dsrc = reinterpret_cast<const char*>(dbase + (int64_t)qrow0 * D);
+    cp.ssrc = lane < C::QS ? lbase + qrow0 + lane : ebase + qrow0 + (lane - C::QS);
+    return cp;
+  };
+  // piece p of an item's copy into stage stg (p < TP: Q, < 2TP: dO, else stats)
+  auto copy_piece = [&](const Copy& cp, int stg, int p) {
+    if (p < 2 * TP) {
+      const int i = p % TP;
+      const uint32_t lds = smem_lds + (uint32_t)((stg * 2 * C::TILE + (p < TP ? 0 : C::TILE)) * 2) + cp_loff[i];
+      dma16_s(cp_goff[i], p < TP ? cp.qsrc : cp.dsrc, __builtin_amdgcn_readfirstlane(lds));
+    } else {
+      dma4(cp.ssrc, __builtin_amdgcn_readfirstlane(sstat_lds + (uint32_t)(stg * 2 * C::QS * 4)));
     }
   };
 
@@ -270,53 +366,144 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     dvacc[mt] = f32x16{};
   }
 
-  if (items > 0) dma(0, 0);
-  dma_wait();
-  __syncthreads();
-  int stage = 0;
-  for (int it = 0; it < items; ++it) {
-    const bool more = it + 1 < items;
-    if (more) dma(it + 1, stage ^ 1);
-    const T* Qs = smem + stage * C::STAGE;
-    const T* Ds = Qs + C::TILE;
+  auto row_read = [&](int stg, int tilesel, int ks) {
+    return as_vec8<T>(*reinterpret_cast<const u32x4*>(
+        smem_c + row_off[ks] + (stg * 2 * C::TILE + tilesel * C::TILE) * 2));
+  };
+  auto tr_read = [&](int stg, int tilesel, int mt, int j) {
+    const char* base = smem_c + (stg * 2 * C::TILE + tilesel * C::TILE + 16 * j * D) * 2;
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][0]));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][1]));
+    u32x4 rr;
+    rr[0] = __builtin_bit_cast(u32x2, lo)[0];
+    rr[1] = __builtin_bit_cast(u32x2, lo)[1];
+    rr[2] = __builtin_bit_cast(u32x2, hi)[0];
+    rr[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return as_vec8<T>(rr);
+  };
+  auto read_stats = [&](int stg, f32x4 (&l4)[4], f32x4 (&d4)[4], int g) {
+    const char* st = sstat_c + st_off + stg * 2 * C::QS * 4;
+    l4[g] = *reinterpret_cast<const f32x4*>(st + 8 * g * 4);
+    d4[g] = *reinterpret_cast<const f32x4*>(st + (C::QS + 8 * g) * 4);
+  };
 
-    // S = Q K^T and dP = dO V^T: 32 queries x 32 keys
-    f32x16 sacc = f32x16{}, pacc = f32x16{};
+  // Every step copies exactly one item (past the last item it re-copies the
+  // last one into the free stage), so item i+1 has landed once at most NS-3
+  // younger items are in flight.
+  f32x16 sA, pA, sB, pB;
+  f32x4 lA[4], dA[4], lB[4], dB[4];
+  Copy cpn;
+  if (items <= 0) goto epilogue;
+  {
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i) {
+      const Copy cp = copy_of(i < items ? i : items - 1);
+#pragma unroll
+      for (int p = 0; p < C::PER; ++p) copy_piece(cp, i, p);
+    }
+    cpn = copy_of(NS - 1 < items ? NS - 1 : items - 1);
+    wait_vmcnt<(NS - 2) * C::PER>();
+    __syncthreads();
+    sA = f32x16{};
+    pA = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      sacc = E::mfma32(row_a8<T, D>(Qs, r, ks, h), kf[ks], sacc);
-      pacc = E::mfma32(row_a8<T, D>(Ds, r, ks, h), vf[ks], pacc);
+      sA = E::mfma32(row_read(0, 0, ks), kf[ks], sA);
+      pA = E::mfma32(row_read(0, 1, ks), vf[ks], pA);
     }
-    // rows of this lane: queries 8g + 4h + e; consumed 8 queries (g = 2j, 2j+1)
-    // at a time: dV^T += dO^T P ; dK^T += Q^T dS
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float pv[8], dsv[8];
-#pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
-        const int g = 2 * j + gg;
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&sstat[stage][0][8 * g + 4 * h]);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sstat[stage][1][8 * g + 4 * h]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = key_valid ? fast_exp2(fmaf(sacc[4 * g + e], c2, -l4[e])) : 0.f;
-          pv[4 * gg + e] = p;
-          dsv[4 * gg + e] = p * (pacc[4 * g + e] - d4[e]);
-        }
-      }
-      const V8 bp = pack8<T>(pv);
-      const V8 bs = pack8<T>(dsv);
-#pragma unroll
-      for (int mt = 0; mt < D / 32; ++mt) {
-        dvacc[mt] = E::mfma32(tr_a8<T, D>(Ds, mt * 32, 16 * j, 16 * j + 8), bp, dvacc[mt]);
-        dkacc[mt] = E::mfma32(tr_a8<T, D>(Qs, mt * 32, 16 * j, 16 * j + 8), bs, dkacc[mt]);
-      }
-    }
-    dma_wait();
-    __syncthreads();
-    stage ^= 1;
+    for (int g = 0; g < 4; ++g) read_stats(0, lA, dA, g);
   }
 
+  {
+    // One pipeline step on item i (stage S = i % NS): B(i) between the MFMAs
+    // of A(i+1), then C(i).  LDS operands stream with a lookahead of L: rows
+    // of item i+1 for A, then transposed tiles of item i for C, then the
+    // statistics of item i+1.  The copy of item i+NS-1 goes to stage S-1.
+    auto step = [&](auto stage_c, int it, f32x16& sc, f32x16& pc, f32x16& sn, f32x16& pn,
+                    f32x4 (&lc)[4], f32x4 (&dc)[4], f32x4 (&ln)[4], f32x4 (&dn)[4]) {
+      constexpr int S = decltype(stage_c)::value;
+      constexpr int SN = (S + 1) % NS, SP = (S + NS - 1) % NS;
+      wait_vmcnt<(NS - 3) * C::PER>();
+      // publishes item it+1 to every wave and retires every wave's reads of
+      // item it-1, whose stage the copy below reuses
+      __syncthreads();
+      const Copy cp = cpn;
+      V8 op[NA + NC];
+      auto issue = [&](int x) {
+        if (x < NA) {
+          op[x] = row_read(SN, x & 1, x >> 1);
+        } else if (x < NA + NC) {
+          const int vv = x - NA;
+          const int j = vv / (2 * (D / 32)), mt = (vv >> 1) % (D / 32);
+          op[x] = tr_read(S, (vv & 1) ? 0 : 1, mt, j);
+        } else if (x < NA + NC + 4) {
+          read_stats(SN, ln, dn, x - NA - NC);
+        }
+      };
+#pragma unroll
+      for (int x = 0; x < L; ++x) issue(x);
+      sn = f32x16{};
+      pn = f32x16{};
+      float pv[16], dsv[16];
+#pragma unroll
+      for (int u = 0; u < NA; ++u) {
+        issue(u + L);
+#pragma unroll
+        for (int p = 0; p < C::PER; ++p)
+          if ((p * NA) / C::PER == u) copy_piece(cp, SP, p);
+        if (u & 1)
+          pn = E::mfma32(op[u], vf[u >> 1], pn);
+        else
+          sn = E::mfma32(op[u], kf[u >> 1], sn);
+#pragma unroll
+        for (int x = (16 * u) / NA; x < (16 * (u + 1)) / NA; ++x) {
+          pv[x] = fast_exp2(fmaf(sc[x], c2, -lc[x >> 2][x & 3]));
+          if (x >= 1) dsv[x - 1] = pv[x - 1] * (pc[x - 1] - dc[(x - 1) >> 2][(x - 1) & 3]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      dsv[15] = pv[15] * (pc[15] - dc[3][3]);
+      V8 bp[2], bs[2];
+      bp[0] = pack8<T>(pv);
+      bp[1] = pack8<T>(pv + 8);
+      bs[0] = pack8<T>(dsv);
+      bs[1] = pack8<T>(dsv + 8);
+      // descriptor of the copy issued by the next step (its CSR entry is an
+      // LDS read; doing it here keeps it off the next step's critical path)
+      const int nn = it + NS;
+      cpn = copy_of(nn < items ? nn : items - 1);
+#pragma unroll
+      for (int vv = 0; vv < NC; ++vv) {
+        issue(NA + vv + L);
+        const int j = vv / (2 * (D / 32)), mt = (vv >> 1) % (D / 32);
+        if (vv & 1)
+          dkacc[mt] = E::mfma32(op[NA + vv], bs[j], dkacc[mt]);
+        else
+          dvacc[mt] = E::mfma32(op[NA + vv], bp[j], dvacc[mt]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int x = NA + NC + L; x < NA + NC + 4; ++x) issue(x);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    static_assert(NS == 4, "the step sequence below is unrolled for NS = 4");
+    int it = 0;
+    for (; it + 4 <= items; it += 4) {
+      step(I0{}, it, sA, pA, sB, pB, lA, dA, lB, dB);
+      step(I1{}, it + 1, sB, pB, sA, pA, lB, dB, lA, dA);
+      step(I2{}, it + 2, sA, pA, sB, pB, lA, dA, lB, dB);
+      step(I3{}, it + 3, sB, pB, sA, pA, lB, dB, lA, dA);
+    }
+    if (it < items) step(I0{}, it, sA, pA, sB, pB, lA, dA, lB, dB);
+    if (it + 1 < items) step(I1{}, it + 1, sB, pB, sA, pA, lB, dB, lA, dA);
+    if (it + 2 < items) step(I2{}, it + 2, sA, pA, sB, pB, lA, dA, lB, dB);
+  }
+
+epilogue:
   // ---- epilogue ------------------------------------------------------------
   const int32_t cnt = kv_vbs[kvblk];
   const float cdiv = (float)(cnt > 1 ? cnt : 1);
@@ -339,11 +526,15 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
           cv[e] = round_t<T>(E::to_f(va[e]) / cdiv);
         }
       }
+      // A padding key gets no gradient; its lane's accumulators (which only
+      // ever hold that key) are dropped here instead of masking every score.
       T k4[4], v4[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        k4[e] = E::from_f(round_t<T>(dkacc[mt][4 * g + e] * scale) + ck[e]);
-        v4[e] = E::from_f(round_t<T>(dvacc[mt][4 * g + e]) + cv[e]);
+        const float fk = key_valid ? round_t<T>(dkacc[mt][4 * g + e] * scale) : 0.f;
+        const float fv = key_valid ? round_t<T>(dvacc[mt][4 * g + e]) : 0.f;
+        k4[e] = E::from_f(fk + ck[e]);
+        v4[e] = E::from_f(fv + cv[e]);
       }
       *reinterpret_cast<u32x2*>(dk + ktok * D + d0) = *reinterpret_cast<const u32x2*>(k4);
       *reinterpret_cast<u32x2*>(dv + ktok * D + d0) = *reinterpret_cast<const u32x2*>(v4);
