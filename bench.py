@@ -171,7 +171,7 @@ def main():
     ap.add_argument("--kernels-only", action="store_true", help="skip the CPU baseline and summary")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy a 1 GiB buffer 3 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
-    ap.add_argument("--cpu-heads", type=int, default=8,
+    ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of the workload timed on the CPU oracle (one at a time)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3",
                     help="BASELINE configuration to run (c3 is the metric's workload)")
@@ -283,11 +283,15 @@ def main():
     dom_t, dom_f = kt[dom]
     achieved = dom_f / (dom_t * 1e-3) / 1e12
 
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of known size)
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"{dom}_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"{dom}_c3_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for ln in f:
+                if ln.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(ln.split(":", 1)[1].strip())
 
     F_total = 3.5 * F_fwd
     value = F_total / (ms_step * 1e-3) / 1e12

@@ -217,21 +217,6 @@ struct DkvCfg {
   static constexpr int L = 12;                     // LDS operand lookahead
 };
 
-// Keep a lane-dependent value in a register: the compiler would otherwise
-// rematerialise the address arithmetic at every use inside the loop.
-template <typename X>
-__device__ __forceinline__ X opaque(X x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
-// Direct global -> LDS copy with a scalar base and a 32-bit lane offset.
-__device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
-               "s"(lds)
-               : "memory");
-}
-
 template <typename T, int D, int BE>
 __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,

@@ -13,10 +13,9 @@
 //    Because a C tile's per-lane rows are {16j + 4h + 0..3, 16j + 8 + 4h + 0..3}
 //    for acc[8j .. 8j+7], a C tile converted to T can be fed straight back as
 //    the B (or A) operand of a product that reduces over the C tile's rows,
-//    provided the other operand enumerates those rows in the same order.
-//    Sequence-major operands that must be read "down a column" are therefore
-//    stored transposed in LDS with the row order permuted inside each group of
-//    16: position p holds sequence index perm16(p) (see seq_pos16 below).
+//    provided the other operand enumerates those rows in the same order:
+//    tr_a8 below reads a row-major LDS tile "down a column" in exactly that
+//    order with ds_read_b64_tr_b16.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -199,6 +198,22 @@ __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
                : "memory");
 }
 
+// Same as dma16 with a scalar 64-bit base and a 32-bit per-lane byte offset
+// (saddr form: no per-lane 64-bit address arithmetic).
+__device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds)
+               : "memory");
+}
+
+// Keep a lane-dependent value in a register: the compiler would otherwise
+// rematerialise address arithmetic at every use inside a loop.
+template <typename X>
+__device__ __forceinline__ X opaque(X x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -230,57 +245,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Wait for this wave's outstanding vector-memory loads (vmcnt = 0).
 __device__ __forceinline__ void dma_wait() { wait_vmcnt<0>(); }
 
-// Ring depth for a workgroup of `nw` waves whose LDS stage is `stage_bytes`:
-// keep enough workgroups per CU for 8 waves (2 per SIMD) and give each as many
-// stages (min_stages..4) as its share of the 160 KiB LDS holds.
-constexpr int ring_depth(int nw, int stage_bytes, int min_stages = 2) {
-  const int wg_per_cu = 8 / nw;
-  const int budget = (163840 / wg_per_cu) < 131072 ? (163840 / wg_per_cu) : 131072;
-  const int fit = budget / stage_bytes;
-  return fit > 4 ? 4 : (fit < min_stages ? min_stages : fit);
-}
-
-// Ring of NS LDS stages, each filled by PER direct loads per thread: wait
-// until the oldest in-flight stage has landed while `newer` younger stages
-// may stay in flight (newer <= NS - 2).  Vector-memory loads retire in order.
-template <int PER, int NS>
-__device__ __forceinline__ void wait_ring(int newer) {
-  static_assert(NS >= 2 && NS <= 4, "ring depth 2..4");
-  if (NS >= 4 && newer >= 2)
-    wait_vmcnt<(NS >= 4 ? 2 * PER : 0)>();
-  else if (NS >= 3 && newer >= 1)
-    wait_vmcnt<(NS >= 3 ? PER : 0)>();
-  else
-    wait_vmcnt<0>();
-}
-
 // exp2 on the transcendental unit without the libm range fix-ups
 // (results below 2^-126 flush to zero, which softmax weights tolerate).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// ---------------------------------------------------------------------------
-// Transposed-tile bookkeeping.
-//   seq_pos16(s): LDS position (inside a 16-group) of sequence index s, so that
-//   lane half h reading positions 8h .. 8h+7 receives sequence indices
-//   {4h .. 4h+3, 8+4h .. 8+4h+3} -- the rows of a C tile owned by that half.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int group4_pos(int g) {  // g: 4-group inside 16
-  return ((g & 1) << 1) | ((g >> 1) & 1);
-}
-
-// Transpose a 4 (rows) x 8 (cols) block of 16-bit values held as 4 rows of
-// u32x4 into 8 rows of 4 values (u32x2 each): out[c] = {r0[c], r1[c], r2[c], r3[c]}.
-__device__ __forceinline__ void transpose4x8_b16(const u32x4 (&rows)[4], u32x2 (&out)[8]) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    // low halves -> column 2m, high halves -> column 2m+1
-    uint32_t a0 = rows[0][m], a1 = rows[1][m], a2 = rows[2][m], a3 = rows[3][m];
-    out[2 * m][0] = __builtin_amdgcn_perm(a1, a0, 0x05040100u);
-    out[2 * m][1] = __builtin_amdgcn_perm(a3, a2, 0x05040100u);
-    out[2 * m + 1][0] = __builtin_amdgcn_perm(a1, a0, 0x07060302u);
-    out[2 * m + 1][1] = __builtin_amdgcn_perm(a3, a2, 0x07060302u);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Wave / block reductions (wave64)
