@@ -162,6 +162,42 @@ def run_workload(key, steps, warmup):
             "peak_hbm_gib_beyond_inputs": round(peak / 2 ** 30, 3), "steps": steps}
 
 
+def run_tiling(steps, warmup):
+    """tile / untile of a c3-sized token tensor ([1, 40960, 40, 128] bf16 on a
+    20 x 32 x 64 latent in (4, 8, 8) tiles) and of a latent with partial tiles;
+    HBM-bound row moves, reported against the 8 TB/s roof (read + write bytes)."""
+    import torch
+    from vsa import tiling
+    out = {"workload": "tiling", "cases": []}
+    for shape, ts, inner in (((20, 32, 64), (4, 8, 8), (40, 128)),
+                             ((21, 30, 52), (4, 4, 4), (40, 128))):
+        S = math.prod(shape)
+        meta = tiling.build_vsa_metadata(shape, ts, device="cuda")
+        nb, be = math.prod(meta["num_tiles"]), meta["max_block_size"]
+        x = torch.randn(1, S, *inner, device="cuda", dtype=torch.bfloat16)
+        tpi, npi, rev = (meta[k] for k in ("tile_partition_indices", "non_pad_index",
+                                           "reverse_tile_partition_indices"))
+        t = tiling.tile(x, tpi, npi, nb, be)
+        row = 2 * math.prod(inner)
+        for _ in range(warmup):
+            tiling.tile(x, tpi, npi, nb, be)
+            tiling.untile(t, npi, rev)
+        t_ms = _events_time(lambda: tiling.tile(x, tpi, npi, nb, be), steps)
+        u_ms = _events_time(lambda: tiling.untile(t, npi, rev), steps)
+        meta_ms = _events_time(lambda: tiling._metadata.__wrapped__(shape, ts, torch.device("cuda", 0)), steps)
+        t_bytes = S * row + nb * be * row          # read the tokens, write the padded layout
+        u_bytes = 2 * S * row                      # read the real rows, write raster order
+        out["cases"].append({
+            "latent": list(shape), "tile": list(ts), "row_bytes": row, "tokens": S,
+            "padded_rows": nb * be,
+            "tile_ms": round(t_ms, 4), "tile_gbps": round(t_bytes / (t_ms * 1e-3) / 1e9, 1),
+            "tile_frac_hbm": round(t_bytes / (t_ms * 1e-3) / 8e12, 3),
+            "untile_ms": round(u_ms, 4), "untile_gbps": round(u_bytes / (u_ms * 1e-3) / 1e9, 1),
+            "untile_frac_hbm": round(u_bytes / (u_ms * 1e-3) / 8e12, 3),
+            "metadata_ms": round(meta_ms, 4)})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -173,7 +209,7 @@ def main():
                     help="only copy a 1 GiB buffer 3 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of the workload timed on the CPU oracle (one at a time)")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3",
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["tiling"], default="c3",
                     help="BASELINE configuration to run (c3 is the metric's workload)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -195,6 +231,9 @@ def main():
 
     from vsa import mi355x as M
 
+    if args.workload == "tiling":
+        print(json.dumps(run_tiling(args.steps, args.warmup)), flush=True)
+        return
     if args.workload != "c3":
         print(json.dumps(run_workload(args.workload, args.steps, args.warmup)), flush=True)
         return

@@ -171,6 +171,49 @@ int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v, const void*
                         int32_t block_elements, int32_t topk, float scale,
                         int32_t dtype, void* stream);
 
+/*
+ * Tile-layout metadata for a (T, H, W) latent grid and (ts, hs, ws) tiles, in
+ * one pass from the closed form of the raster <-> tile mapping.  Replaces
+ * build_vsa_metadata's index tensors (fastvideo_tiling.py:22-88, 91-127):
+ *   tile_partition_indices[S]  raster token ids in tile-contiguous order
+ *                              (get_tile_partition_indices, 22-42);
+ *   reverse_indices[S]         its inverse permutation (45-52);
+ *   non_pad_index[S]           padded slot n*ts*hs*ws + p of each of them (81-88);
+ *   variable_block_sizes[nb]   real tokens per tile (55-78),
+ * with S = T*H*W and nb = ceil(T/ts)*ceil(H/hs)*ceil(W/ws); all int64.
+ */
+int vsa_tile_metadata(int32_t T, int32_t H, int32_t W, int32_t ts, int32_t hs, int32_t ws,
+                      int64_t* tile_partition_indices, int64_t* reverse_indices,
+                      int64_t* non_pad_index, int64_t* variable_block_sizes, void* stream);
+
+/*
+ * Indexed row move along dim 1 of x [batch, x_rows, row] -> out [batch,
+ * out_rows, row], rows of row_bytes bytes (any element type):
+ *   for i < n:  s = src_outer ? src[src_outer[i]] : (src ? src[i] : i)
+ *               d = dst_outer ? dst[dst_outer[i]] : (dst ? dst[i] : i)
+ *               out[b, d, :] = x[b, s, :]
+ * Index values outside their table / the row range are skipped.  With
+ * vsa_rows_zero_unmarked it replaces tile's `buf[:, non_pad_index] =
+ * x[:, tile_partition_indices]` (fastvideo_tiling.py:137-139), untile's
+ * `x[:, non_pad_index][:, reverse]` (145) and the gradients autograd takes
+ * through them.  Duplicate destinations race (the indices of a tiling never
+ * repeat).
+ */
+int vsa_rows_move(const void* x, int64_t x_rows, void* out, int64_t out_rows, int64_t batch,
+                  int64_t row_bytes, const int64_t* src, int64_t src_len,
+                  const int64_t* src_outer, const int64_t* dst, int64_t dst_len,
+                  const int64_t* dst_outer, int64_t n, void* stream);
+
+/*
+ * Zero every row of out [batch, out_rows, row] whose index is not listed in
+ * marked[n_marked]: the zero padding of tile's `torch.zeros` buffer
+ * (fastvideo_tiling.py:137-138) without writing the rows the move fills.
+ * mark_workspace: caller-owned, out_rows bytes.
+ */
+int vsa_rows_zero_unmarked(void* out, int64_t out_rows, int64_t batch, int64_t row_bytes,
+                           const int64_t* marked, int64_t n_marked, uint8_t* mark_workspace,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

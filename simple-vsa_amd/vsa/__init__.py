@@ -2,11 +2,15 @@
 
 Importing ``vsa`` needs only torch; the gfx950 kernel library is loaded on the
 first call, as the reference loads its GPU backends (vsa/__init__.py:28-69).
+The tiling helpers keep the reference's names (vsa/__init__.py:7, 23-24).
 """
 
 from typing import Any
 
-__all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_route"]
+from .tiling import build_vsa_metadata, tile, untile
+
+__all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_route", "build_vsa_metadata", "tile",
+           "untile"]
 
 
 def mi355x_vsa(*args: Any, **kwargs: Any) -> Any:
