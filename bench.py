@@ -198,6 +198,39 @@ def run_tiling(steps, warmup):
     return out
 
 
+def run_gate(steps, warmup):
+    """c3 with the gate produced by CompressionGate(dim=5120, heads=40) from
+    hidden states [1, 40960, 5120]: fwd+bwd of (gate GEMM + mi355x_vsa) with the
+    gate consumed in the producer's token-major layout, against the same step
+    with the gate made contiguous first (what a [B,H,S,D]-only op needs)."""
+    import torch
+    from vsa import CompressionGate
+    from vsa import mi355x as M
+    B, H, S, D, topk = CFG["B"], CFG["H"], CFG["S"], CFG["D"], CFG["topk"]
+    be = math.prod(CFG["block"])
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+                   for _ in range(4))
+    hidden = torch.randn(B, S, H * D, generator=g, device=dev, dtype=torch.bfloat16)
+    layer = CompressionGate(H * D, H).to(dev, torch.bfloat16)
+    vbs = torch.full((S // be,), be, device=dev, dtype=torch.int32)
+    leaves = [t.requires_grad_() for t in (q, k, v)] + list(layer.parameters())
+    res = {"workload": "gate", "gemm_tflop": 2 * B * S * (H * D) ** 2 / 1e12}
+    for name, contiguous in (("token_major", False), ("contiguous_copy", True)):
+        def step():
+            gate = layer(hidden)
+            if contiguous:
+                gate = gate.contiguous()
+            out = M.mi355x_vsa(q, k, v, vbs, vbs, topk, CFG["block"], gate)
+            torch.autograd.grad(out, leaves, do)
+        for _ in range(warmup):
+            step()
+        res[name + "_ms"] = round(_events_time(step, steps), 3)
+    res["saved_ms"] = round(res["contiguous_copy_ms"] - res["token_major_ms"], 3)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -209,7 +242,7 @@ def main():
                     help="only copy a 1 GiB buffer 3 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of the workload timed on the CPU oracle (one at a time)")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["tiling"], default="c3",
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["tiling", "gate"], default="c3",
                     help="BASELINE configuration to run (c3 is the metric's workload)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -231,6 +264,9 @@ def main():
 
     from vsa import mi355x as M
 
+    if args.workload == "gate":
+        print(json.dumps(run_gate(args.steps, args.warmup)), flush=True)
+        return
     if args.workload == "tiling":
         print(json.dumps(run_tiling(args.steps, args.warmup)), flush=True)
         return

@@ -34,8 +34,18 @@ extern "C" {
 
 enum vsa_dtype { VSA_BF16 = 0, VSA_F16 = 1, VSA_F32 = 2 };
 
-/* How compress_attn_weight is laid out: absent, [BH, Sq, D], or [BH, Sq, 1]. */
-enum vsa_gate_mode { VSA_GATE_NONE = 0, VSA_GATE_FULL = 1, VSA_GATE_PER_TOKEN = 2 };
+/*
+ * How compress_attn_weight is laid out: absent, [BH, Sq, D], [BH, Sq, 1], or
+ * token-major [B, Sq, H, D] -- the gate producer's Linear output before its
+ * per-head transpose (common.py:326-328), read and written in place; H is the
+ * `gate_heads` argument and bh = b*H + h.
+ */
+enum vsa_gate_mode {
+  VSA_GATE_NONE = 0,
+  VSA_GATE_FULL = 1,
+  VSA_GATE_PER_TOKEN = 2,
+  VSA_GATE_TOKEN_MAJOR = 3
+};
 
 enum vsa_status {
   VSA_OK = 0,
@@ -113,7 +123,7 @@ int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
 int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                    const int32_t* selected, const int32_t* kv_vbs,
                    void* out, float* lse, const void* out_c, const void* gate,
-                   int32_t gate_mode, int64_t bh, int64_t sq, int64_t skv,
+                   int32_t gate_mode, int32_t gate_heads, int64_t bh, int64_t sq, int64_t skv,
                    int32_t head_dim, int32_t block_elements, int32_t topk,
                    float scale, int32_t dtype, void* stream);
 
@@ -124,10 +134,11 @@ int vsa_sparse_fwd(const void* q, const void* k, const void* v,
  *   attn  = out - out_c[block] * gate    (attn = out when out_c == NULL)
  *   delta[bh, q]   = sum_d attn * dout                               (fp32)
  *   d_out_c[bh, n] = T(sum_{t < be} T(dout * gate))     (if out_c != NULL)
- *   d_gate         = T(dout * out_c[block])  (per token: summed over d)
+ *   d_gate         = T(dout * out_c[block])  (per token: summed over d),
+ * d_gate in the gate's own layout (token-major included).
  */
 int vsa_bwd_prep(const void* out, const void* dout, const void* out_c, const void* gate,
-                 int32_t gate_mode, float* delta, void* d_out_c, void* d_gate,
+                 int32_t gate_mode, int32_t gate_heads, float* delta, void* d_out_c, void* d_gate,
                  int64_t bh, int64_t sq, int32_t head_dim, int32_t block_elements,
                  int32_t dtype, void* stream);
 

@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) void csr_sort_kernel(const int32_t* __restrict
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const T* __restrict__ out, const T* __restrict__ dout, const T* __restrict__ outc,
-    const T* __restrict__ gate, int gate_mode, float* __restrict__ delta,
+    const T* __restrict__ gate, int gate_mode, int gate_heads, float* __restrict__ delta,
     T* __restrict__ d_outc, T* __restrict__ d_gate, int qb, int D, int be) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float part[256 * VEC];
@@ -280,16 +280,26 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     oc[e] = outc ? Elem<T>::to_f(outc[blk * D + c0 + e]) : 0.f;
     dacc[e] = 0.f;
   }
+  // token-major gate [B, Sq, H, D]: element (bh = b*H + h, s, d) at ((b*Sq + s)*H + h)*D + d
+  const int64_t bh = blockIdx.y;
+  const int64_t sq = (int64_t)qb * be;
+  const int64_t gbase = gate_mode == 3
+                            ? ((bh / gate_heads) * sq * gate_heads + bh % gate_heads) * D + c0
+                            : 0;
   for (int t = row0; t < be; t += rpi) {
     const int64_t tok = blk * be + t;
     const int64_t off = tok * D + c0;
+    // offset of this token's gate (and d_gate) chunk
+    const int64_t goff = gate_mode == 3
+                             ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
+                             : off;
     u32x4 ro = *reinterpret_cast<const u32x4*>(out + off);
     u32x4 rd = *reinterpret_cast<const u32x4*>(dout + off);
     const T* o = reinterpret_cast<const T*>(&ro);
     const T* g = reinterpret_cast<const T*>(&rd);
     float gv[VEC];
-    if (gate_mode == 1) {
-      u32x4 rg = *reinterpret_cast<const u32x4*>(gate + off);
+    if (gate_mode == 1 || gate_mode == 3) {
+      u32x4 rg = *reinterpret_cast<const u32x4*>(gate + goff);
       const T* gg = reinterpret_cast<const T*>(&rg);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) gv[e] = Elem<T>::to_f(gg[e]);
@@ -306,8 +316,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       dl = fmaf(attn, dov, dl);
       if (outc) {
         dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[e]);
-        if (gate_mode == 1)
-          d_gate[off + e] = Elem<T>::from_f(dov * oc[e]);
+        if (gate_mode == 1 || gate_mode == 3)
+          d_gate[goff + e] = Elem<T>::from_f(dov * oc[e]);
         else
           dg = fmaf(dov, oc[e], dg);
       }
@@ -496,11 +506,12 @@ extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* 
 }
 
 extern "C" int vsa_bwd_prep(const void* out, const void* dout, const void* out_c,
-                            const void* gate, int32_t gate_mode, float* delta, void* d_out_c,
-                            void* d_gate, int64_t bh, int64_t sq, int32_t D, int32_t be,
-                            int32_t dtype, void* stream) {
+                            const void* gate, int32_t gate_mode, int32_t gate_heads,
+                            float* delta, void* d_out_c, void* d_gate, int64_t bh, int64_t sq,
+                            int32_t D, int32_t be, int32_t dtype, void* stream) {
   if (!out || !dout || !delta) return VSA_ERR_NULL;
-  if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;
+  if (gate_mode < 0 || gate_mode > 3) return VSA_ERR_SHAPE;
+  if (out_c && gate_mode == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
   if (out_c && !d_out_c) return VSA_ERR_NULL;
   if (out_c && gate_mode != 0 && (!gate || !d_gate)) return VSA_ERR_NULL;
   if (!out_c) gate_mode = 0;
@@ -510,7 +521,7 @@ extern "C" int vsa_bwd_prep(const void* out, const void* dout, const void* out_c
   VSA_DISPATCH_ALL(dtype, T, {
     hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3(qb, (unsigned)bh), dim3(256), 0, s,
                        (const T*)out, (const T*)dout, (const T*)out_c, (const T*)gate, gate_mode,
-                       delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
+                       gate_heads, delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
   });
   return vsa_check_launch();
 }

@@ -61,7 +61,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
-    const T* __restrict__ gate, int gate_mode, int num_tiles, int tiles_per_head, int sq,
+    const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles, int tiles_per_head, int sq,
     int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
   using C = FwdCfg<D, BE>;
   using E = Elem<T>;
@@ -194,6 +194,11 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   const T* ocrow = outc ? outc + ((int64_t)b * qb + qblk) * D : nullptr;
   float gtok = 1.f;
   if (outc && gate_mode == 2) gtok = E::to_f(gate[tok]);
+  // gate row of this token: [BH, Sq, D] (mode 1) or token-major [B, Sq, H, D] (mode 3)
+  const T* grow = nullptr;
+  if (gate_mode == 1) grow = gate + tok * D;
+  if (gate_mode == 3)
+    grow = gate + (((int64_t)(b / gate_heads) * sq + myq) * gate_heads + b % gate_heads) * D;
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) {
 #pragma unroll
@@ -206,8 +211,8 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
         u32x2 ocr = *reinterpret_cast<const u32x2*>(ocrow + d0);
         const T* oc = reinterpret_cast<const T*>(&ocr);
         float gv[4] = {gtok, gtok, gtok, gtok};
-        if (gate_mode == 1) {
-          u32x2 gr = *reinterpret_cast<const u32x2*>(gate + tok * D + d0);
+        if (grow) {
+          u32x2 gr = *reinterpret_cast<const u32x2*>(grow + d0);
           const T* gg = reinterpret_cast<const T*>(&gr);
 #pragma unroll
           for (int e = 0; e < 4; ++e) gv[e] = E::to_f(gg[e]);
@@ -226,7 +231,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 template <typename T, int D, int BE>
 static int launch_fwd(const void* q, const void* k, const void* v, const int32_t* selected,
                       const int32_t* kv_vbs, void* out, float* lse, const void* outc,
-                      const void* gate, int gate_mode, int64_t bh, int64_t sq, int64_t skv,
+                      const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq, int64_t skv,
                       int topk, float scale, hipStream_t stream) {
   using C = FwdCfg<D, BE>;
   const int tph = (int)(sq / C::QT);
@@ -237,7 +242,7 @@ static int launch_fwd(const void* q, const void* k, const void* v, const int32_t
   const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
   hipLaunchKernelGGL((sparse_fwd_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, lse,
-                     (const T*)outc, (const T*)gate, gate_mode, (int)tiles, tph, (int)sq,
+                     (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, tph, (int)sq,
                      (int)skv, (int)(sq / BE), (int)(skv / BE), topk, c2, qsign);
   return vsa_check_launch();
 }
@@ -248,16 +253,17 @@ using namespace vsa;
 
 #define VSA_FWD_CASE(DD, BB)                                                                   \
   if (D == DD && be == BB)                                                                     \
-    return launch_fwd<T, DD, BB>(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode, \
+    return launch_fwd<T, DD, BB>(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode, gate_heads, \
                                  bh, sq, skv, topk, scale, s);
 
 extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                               const int32_t* selected, const int32_t* kv_vbs, void* out,
                               float* lse, const void* out_c, const void* gate, int32_t gate_mode,
-                              int64_t bh, int64_t sq, int64_t skv, int32_t D, int32_t be,
-                              int32_t topk, float scale, int32_t dtype, void* stream) {
+                              int32_t gate_heads, int64_t bh, int64_t sq, int64_t skv, int32_t D,
+                              int32_t be, int32_t topk, float scale, int32_t dtype, void* stream) {
   if (!q || !k || !v || !selected || !kv_vbs || !out) return VSA_ERR_NULL;
-  if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;
+  if (gate_mode < 0 || gate_mode > 3) return VSA_ERR_SHAPE;
+  if (out_c && gate_mode == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
   if (out_c && gate_mode != 0 && !gate) return VSA_ERR_NULL;
   if (!out_c) gate_mode = 0;
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||

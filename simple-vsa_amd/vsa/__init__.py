@@ -2,15 +2,17 @@
 
 Importing ``vsa`` needs only torch; the gfx950 kernel library is loaded on the
 first call, as the reference loads its GPU backends (vsa/__init__.py:28-69).
-The tiling helpers keep the reference's names (vsa/__init__.py:7, 23-24).
+The tiling helpers and the gate producer keep the reference's names
+(vsa/__init__.py:7, 10-25).
 """
 
 from typing import Any
 
+from .gate import CompressionGate
 from .tiling import build_vsa_metadata, tile, untile
 
-__all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_route", "build_vsa_metadata", "tile",
-           "untile"]
+__all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_route", "CompressionGate",
+           "build_vsa_metadata", "tile", "untile"]
 
 
 def mi355x_vsa(*args: Any, **kwargs: Any) -> Any:

@@ -18,7 +18,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libvsa_mi355x.so")
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
-GATE_NONE, GATE_FULL, GATE_PER_TOKEN = 0, 1, 2
+GATE_NONE, GATE_FULL, GATE_PER_TOKEN, GATE_TOKEN_MAJOR = 0, 1, 2, 3
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -33,9 +33,9 @@ SIGNATURES = {
     "vsa_coarse_fwd": [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _F, _I32, _P],
     "vsa_topk": [_P, _P, _I64, _I32, _I32, _P],
     "vsa_csr_build": [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P],
-    "vsa_sparse_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I32, _I32,
-                       _I32, _F, _I32, _P],
-    "vsa_bwd_prep": [_P, _P, _P, _P, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P],
+    "vsa_sparse_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I64, _I64, _I64, _I32,
+                       _I32, _I32, _F, _I32, _P],
+    "vsa_bwd_prep": [_P, _P, _P, _P, _I32, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P],
     "vsa_coarse_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F, _I32, _P],
     "vsa_sparse_bwd_dq": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I32,
                           _I32, _I32, _F, _I32, _P],

@@ -158,13 +158,27 @@ def sparse_forward(q, k, v, selected, variable_block_sizes, block_elements, scal
     skv = k.shape[2]
     out = torch.empty_like(q)
     lse = (torch.empty((b, h, sq), device=q.device, dtype=torch.float32) if want_lse else None)
-    gmode = _lib.GATE_NONE if (out_c is None or gate is None) else (
-        _lib.GATE_PER_TOKEN if gate.shape[-1] == 1 and d != 1 else _lib.GATE_FULL)
+    gmode = _gate_mode(gate, d) if out_c is not None else _lib.GATE_NONE
     _lib.call("vsa_sparse_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(selected),
               _lib.ptr(variable_block_sizes), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(out_c),
-              _lib.ptr(gate if gmode else None), gmode, b * h, sq, skv, d, block_elements,
+              _lib.ptr(gate if gmode else None), gmode, h, b * h, sq, skv, d, block_elements,
               selected.shape[-1], float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
     return out, lse
+
+
+def _token_major(gate: Tensor) -> bool:
+    """True when a [B, H, S, D] gate is the per-head transpose of a contiguous
+    [B, S, H, D] tensor (the gate producer's Linear output, common.py:326-328)."""
+    b, h, s, d = gate.shape
+    return gate.stride() == (s * h * d, d, h * d, 1) and not gate.is_contiguous()
+
+
+def _gate_mode(gate: Optional[Tensor], d: int) -> int:
+    if gate is None:
+        return _lib.GATE_NONE
+    if gate.shape[-1] == 1 and d != 1:
+        return _lib.GATE_PER_TOKEN
+    return _lib.GATE_TOKEN_MAJOR if _token_major(gate) else _lib.GATE_FULL
 
 
 def backward_prep(out, dout, block_elements, *, out_c=None, gate=None):
@@ -172,11 +186,14 @@ def backward_prep(out, dout, block_elements, *, out_c=None, gate=None):
     b, h, sq, d = out.shape
     delta = torch.empty((b, h, sq), device=out.device, dtype=torch.float32)
     d_outc = torch.empty_like(out_c) if out_c is not None else None
-    gmode = _lib.GATE_NONE if (out_c is None or gate is None) else (
-        _lib.GATE_PER_TOKEN if gate.shape[-1] == 1 and d != 1 else _lib.GATE_FULL)
-    d_gate = torch.empty_like(gate) if gmode else None
+    gmode = _gate_mode(gate, d) if out_c is not None else _lib.GATE_NONE
+    d_gate = None
+    if gmode == _lib.GATE_TOKEN_MAJOR:   # gradient in the gate's own token-major layout
+        d_gate = torch.empty((b, sq, h, d), device=gate.device, dtype=gate.dtype).transpose(1, 2)
+    elif gmode:
+        d_gate = torch.empty_like(gate, memory_format=torch.contiguous_format)
     _lib.call("vsa_bwd_prep", _lib.ptr(out), _lib.ptr(dout), _lib.ptr(out_c),
-              _lib.ptr(gate if gmode else None), gmode, _lib.ptr(delta), _lib.ptr(d_outc),
+              _lib.ptr(gate if gmode else None), gmode, h, _lib.ptr(delta), _lib.ptr(d_outc),
               _lib.ptr(d_gate), b * h, sq, d, block_elements, _lib.dtype_code(out.dtype),
               _lib.stream_of(out))
     return delta, d_outc, d_gate
@@ -305,7 +322,9 @@ def _prepare_gate(gate: Optional[Tensor], q: Tensor) -> Optional[Tensor]:
     if tuple(gate.shape) not in ((b, h, s, d), (b, h, s, 1)):
         raise ValueError(
             "compress_attn_weight must have the same shape as q, or [batch, heads, seq_len, 1]")
-    return gate.to(device=q.device, dtype=q.dtype).contiguous()
+    gate = gate.to(device=q.device, dtype=q.dtype)
+    # the gate producer's per-head view of its [B, S, H, D] output is consumed in place
+    return gate if _token_major(gate) else gate.contiguous()
 
 
 def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,

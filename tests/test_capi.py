@@ -52,12 +52,22 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     p = _lib.ptr(torch.zeros(1))
     assert lib.vsa_topk(p, p, 1, 4, 5, None) == -2          # topk > Kb
     assert lib.vsa_csr_build(p, p, p, p, 1, 4, 0, 2, None) == -2
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
                               1, 100, 128, 128, 64, 1, 0.1, 0, None) == -2   # 100 % 64
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
                               1, 96, 96, 128, 96, 1, 0.1, 0, None) == -4     # be 96: no kernel
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
                               1, 64, 64, 128, 64, 1, 0.1, 2, None) == -3     # fp32 on MFMA path
+    # token-major gate: the heads count must divide batch*heads
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, p, p, 3, 3,
+                              4, 64, 64, 128, 64, 1, 0.1, 0, None) == -2
+    assert lib.vsa_bwd_prep(p, p, p, p, 3, 0, p, p, p, 4, 64, 128, 64, 0, None) == -2
+    # tiling entry points validate before launching
+    assert lib.vsa_tile_metadata(0, 4, 4, 2, 2, 2, p, p, p, p, None) == -2
+    assert lib.vsa_tile_metadata(4, 4, 4, 2, 2, 2, None, p, p, p, None) == -1
+    assert lib.vsa_rows_move(None, 4, p, 4, 1, 16, None, 0, None, None, 0, None, 4, None) == -1
+    assert lib.vsa_rows_move(p, 4, p, 4, 1, 0, None, 0, None, None, 0, None, 4, None) == -2
+    assert lib.vsa_rows_zero_unmarked(p, 4, 1, 16, None, 2, p, None) == -1
 
 
 def _full(nb, be):

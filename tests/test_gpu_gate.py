@@ -1,0 +1,85 @@
+"""GPU parity of the gate-producer row: the token-major gate path of
+mi355x_vsa (gate read and its gradient written in the Linear's own layout)."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import vsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _gpu_only():
+    if not torch.cuda.is_available():
+        pytest.skip("needs an MI355X")
+    from vsa import _lib
+    _lib.load()
+    yield
+
+
+def _grads(q, k, v, gate, vbs, topk, block, do):
+    from vsa import mi355x as M
+    leaves = [t.detach().clone().requires_grad_() for t in (q, k, v)]
+    g = gate.detach().clone() if gate.is_contiguous() else \
+        gate.detach().transpose(1, 2).clone().transpose(1, 2)
+    g.requires_grad_()
+    out = M.mi355x_vsa(*leaves, vbs, vbs, topk, block, g)
+    grads = torch.autograd.grad(out, leaves + [g], do)
+    return out.detach(), grads
+
+
+@pytest.mark.parametrize("B,H,S,D,be,topk", [(2, 3, 1024, 64, 64, 4), (1, 4, 2048, 128, 256, 3),
+                                              (1, 40, 40960, 128, 256, 20)])
+def test_token_major_gate_is_bit_identical_to_contiguous_gate(B, H, S, D, be, topk):
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=gen, device=DEV, dtype=torch.bfloat16)
+                   for _ in range(4))
+    # the producer's layout: [B, S, H, D] contiguous, viewed per head
+    g_tm = torch.rand(B, S, H, D, generator=gen, device=DEV, dtype=torch.bfloat16).transpose(1, 2)
+    from vsa import mi355x as M
+    assert M._token_major(g_tm)
+    vbs = torch.full((S // be,), be, device=DEV, dtype=torch.int32)
+    vbs[-1] = be - 7
+    out_a, gr_a = _grads(q, k, v, g_tm, vbs, topk, (1, 1, be), do)
+    out_b, gr_b = _grads(q, k, v, g_tm.contiguous(), vbs, topk, (1, 1, be), do)
+    assert torch.equal(out_a, out_b)
+    for a, b in zip(gr_a, gr_b):
+        assert torch.equal(a.contiguous(), b.contiguous())
+    # the gate gradient keeps the producer's layout (no transpose copy)
+    assert M._token_major(gr_a[3])
+
+
+def test_gate_producer_trains_end_to_end_against_oracle():
+    from vsa import CompressionGate
+    from vsa import mi355x as M
+    torch.manual_seed(1)
+    B, H, D, be, nb = 1, 2, 64, 64, 6
+    S, dim = be * nb, H * D
+    hidden = torch.randn(B, S, dim)
+    q, k, v = (torch.randn(B, H, S, D) for _ in range(3))
+    layer = CompressionGate(dim=dim, num_heads=H)
+    vbs = torch.full((nb,), be, dtype=torch.int32)
+    # GPU: bf16 Linear (hipBLASLt) + mi355x_vsa, token-major gate
+    lg = CompressionGate(dim=dim, num_heads=H).to(DEV, torch.bfloat16)
+    lg.load_state_dict(layer.state_dict())
+    gate = lg(hidden.to(DEV, torch.bfloat16))
+    assert M._token_major(gate)
+    out = M.mi355x_vsa(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16),
+                       v.to(DEV, torch.bfloat16), vbs.to(DEV), vbs.to(DEV), 2, (1, 1, be), gate)
+    out.float().square().mean().backward()
+    gw = lg.to_gate_compress.weight.grad
+    assert gw is not None and torch.isfinite(gw).all() and gw.abs().sum() > 0
+    # oracle: same weights in fp32 on the CPU, bf16 inputs, the GPU's route
+    _, sel = M.mi355x_route(q.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16),
+                            v.to(DEV, torch.bfloat16), vbs.to(DEV), vbs.to(DEV), 2, (1, 1, be))
+    rg = layer(hidden.to(torch.bfloat16).float())
+    ro = O.torch_vsa(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), vbs, vbs,
+                     2, (1, 1, be), rg.to(torch.bfloat16), selected=sel.cpu().long())
+    ro.float().square().mean().backward()
+    rw = layer.to_gate_compress.weight.grad
+    rel = ((gw.float().cpu() - rw).norm() / rw.norm()).item()
+    assert rel < 3e-2, rel
