@@ -198,22 +198,25 @@ int vsa_tile_metadata(int32_t T, int32_t H, int32_t W, int32_t ts, int32_t hs, i
                       int64_t* non_pad_index, int64_t* variable_block_sizes, void* stream);
 
 /*
- * Indexed row move along dim 1 of x [batch, x_rows, row] -> out [batch,
- * out_rows, row], rows of row_bytes bytes (any element type):
+ * Indexed row move along dim 1 of x [batch, x_rows, x_row_bytes] -> out
+ * [batch, out_rows, out_row_bytes] (any element type):
  *   for i < n:  s = src_outer ? src[src_outer[i]] : (src ? src[i] : i)
  *               d = dst_outer ? dst[dst_outer[i]] : (dst ? dst[i] : i)
- *               out[b, d, :] = x[b, s, :]
- * Index values outside their table / the row range are skipped.  With
+ *               out[b, d, :copy_bytes] = x[b, s, :copy_bytes]
+ *               out[b, d, copy_bytes:] = 0
+ * (copy_bytes <= both row lengths; unequal row lengths pad or crop the last
+ * dimension).  Index values outside their table / the row range are skipped.  With
  * vsa_rows_zero_unmarked it replaces tile's `buf[:, non_pad_index] =
  * x[:, tile_partition_indices]` (fastvideo_tiling.py:137-139), untile's
  * `x[:, non_pad_index][:, reverse]` (145) and the gradients autograd takes
  * through them.  Duplicate destinations race (the indices of a tiling never
  * repeat).
  */
-int vsa_rows_move(const void* x, int64_t x_rows, void* out, int64_t out_rows, int64_t batch,
-                  int64_t row_bytes, const int64_t* src, int64_t src_len,
-                  const int64_t* src_outer, const int64_t* dst, int64_t dst_len,
-                  const int64_t* dst_outer, int64_t n, void* stream);
+int vsa_rows_move(const void* x, int64_t x_rows, int64_t x_row_bytes, void* out,
+                  int64_t out_rows, int64_t out_row_bytes, int64_t copy_bytes, int64_t batch,
+                  const int64_t* src, int64_t src_len, const int64_t* src_outer,
+                  const int64_t* dst, int64_t dst_len, const int64_t* dst_outer, int64_t n,
+                  void* stream);
 
 /*
  * Zero every row of out [batch, out_rows, row] whose index is not listed in

@@ -77,14 +77,17 @@ template <> struct Vec<4> { typedef uint32_t t; };
 template <> struct Vec<2> { typedef uint16_t t; };
 template <> struct Vec<1> { typedef uint8_t t; };
 
-// Rows of `row_bytes` bytes, TPR threads per row (power of two), 256 threads
-// per workgroup; blockIdx.y walks the batch.
+// Row moves, TPR threads per row (power of two), 256 threads per workgroup;
+// blockIdx.y walks the batch.  Rows are counted in VB-byte chunks: x rows are
+// xc chunks long, out rows oc, the first cc chunks are copied and chunks
+// [cc, oc) of the destination row are zeroed.
 template <int VB>
 __global__ __launch_bounds__(256) void rows_move_kernel(
-    const char* __restrict__ x, int64_t x_rows, char* __restrict__ out, int64_t out_rows,
-    int64_t batch, int64_t cpr, int tpr_log2, const int64_t* __restrict__ src,
-    int64_t src_len, const int64_t* __restrict__ src_outer, const int64_t* __restrict__ dst,
-    int64_t dst_len, const int64_t* __restrict__ dst_outer, int64_t n) {
+    const char* __restrict__ x, int64_t x_rows, int64_t xc, char* __restrict__ out,
+    int64_t out_rows, int64_t oc, int64_t cc, int64_t batch, int tpr_log2,
+    const int64_t* __restrict__ src, int64_t src_len, const int64_t* __restrict__ src_outer,
+    const int64_t* __restrict__ dst, int64_t dst_len, const int64_t* __restrict__ dst_outer,
+    int64_t n) {
   typedef typename Vec<VB>::t V;
   const int tpr = 1 << tpr_log2;
   const int64_t i = (int64_t)blockIdx.x * (256 >> tpr_log2) + (threadIdx.x >> tpr_log2);
@@ -94,9 +97,9 @@ __global__ __launch_bounds__(256) void rows_move_kernel(
   const int64_t d = lookup(dst, dst_len, dst_outer, i);
   if (s < 0 || s >= x_rows || d < 0 || d >= out_rows) return;
   for (int64_t b = blockIdx.y; b < batch; b += gridDim.y) {
-    const V* sp = reinterpret_cast<const V*>(x + (b * x_rows + s) * cpr * VB);
-    V* dp = reinterpret_cast<V*>(out + (b * out_rows + d) * cpr * VB);
-    for (int64_t c = lane; c < cpr; c += tpr) dp[c] = sp[c];
+    const V* sp = reinterpret_cast<const V*>(x + (b * x_rows + s) * xc * VB);
+    V* dp = reinterpret_cast<V*>(out + (b * out_rows + d) * oc * VB);
+    for (int64_t c = lane; c < oc; c += tpr) dp[c] = c < cc ? sp[c] : V{};
   }
 }
 
@@ -129,11 +132,12 @@ __global__ __launch_bounds__(256) void rows_zero_kernel(char* __restrict__ out, 
   }
 }
 
-// Widest vector that divides the row and keeps every row start aligned.
-static int vec_bytes(int64_t row_bytes, const void* a, const void* b) {
+// Widest vector that divides every row length and keeps every row start aligned.
+static int vec_bytes(int64_t a_bytes, int64_t b_bytes, int64_t c_bytes, const void* a,
+                     const void* b) {
   const uintptr_t al = (uintptr_t)a | (uintptr_t)b;
   for (int vb = 16; vb > 1; vb >>= 1)
-    if (row_bytes % vb == 0 && al % vb == 0) return vb;
+    if (a_bytes % vb == 0 && b_bytes % vb == 0 && c_bytes % vb == 0 && al % vb == 0) return vb;
   return 1;
 }
 
@@ -179,24 +183,26 @@ extern "C" int vsa_tile_metadata(int32_t T, int32_t H, int32_t W, int32_t ts, in
   return vsa_check_launch();
 }
 
-extern "C" int vsa_rows_move(const void* x, int64_t x_rows, void* out, int64_t out_rows,
-                             int64_t batch, int64_t row_bytes, const int64_t* src,
-                             int64_t src_len, const int64_t* src_outer, const int64_t* dst,
-                             int64_t dst_len, const int64_t* dst_outer, int64_t n,
-                             void* stream) {
+extern "C" int vsa_rows_move(const void* x, int64_t x_rows, int64_t x_row_bytes, void* out,
+                             int64_t out_rows, int64_t out_row_bytes, int64_t copy_bytes,
+                             int64_t batch, const int64_t* src, int64_t src_len,
+                             const int64_t* src_outer, const int64_t* dst, int64_t dst_len,
+                             const int64_t* dst_outer, int64_t n, void* stream) {
   if (!x || !out) return VSA_ERR_NULL;
   if ((src_outer && !src) || (dst_outer && !dst)) return VSA_ERR_NULL;
-  if (x_rows < 0 || out_rows < 0 || batch < 0 || row_bytes <= 0 || n < 0) return VSA_ERR_SHAPE;
+  if (x_rows < 0 || out_rows < 0 || batch < 0 || n < 0 || copy_bytes <= 0 ||
+      copy_bytes > x_row_bytes || copy_bytes > out_row_bytes)
+    return VSA_ERR_SHAPE;
   if (n == 0 || batch == 0) return VSA_OK;
-  const int vb = vec_bytes(row_bytes, x, out);
-  const int64_t cpr = row_bytes / vb;
-  const int tl = tpr_log2_for(cpr);
+  const int vb = vec_bytes(x_row_bytes, out_row_bytes, copy_bytes, x, out);
+  const int64_t xc = x_row_bytes / vb, oc = out_row_bytes / vb, cc = copy_bytes / vb;
+  const int tl = tpr_log2_for(oc);
   dim3 grid;
   if (!row_grid(n, tl, batch, grid)) return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
 #define VSA_MOVE(VB)                                                                          \
-  hipLaunchKernelGGL(rows_move_kernel<VB>, grid, dim3(256), 0, s, (const char*)x, x_rows,     \
-                     (char*)out, out_rows, batch, cpr, tl, src, src_len, src_outer, dst,     \
+  hipLaunchKernelGGL(rows_move_kernel<VB>, grid, dim3(256), 0, s, (const char*)x, x_rows, xc, \
+                     (char*)out, out_rows, oc, cc, batch, tl, src, src_len, src_outer, dst,   \
                      dst_len, dst_outer, n)
   switch (vb) {
     case 16: VSA_MOVE(16); break;
@@ -222,7 +228,7 @@ extern "C" int vsa_rows_zero_unmarked(void* out, int64_t out_rows, int64_t batch
   if (n_marked > 0)
     hipLaunchKernelGGL(mark_set_kernel, dim3((unsigned)((n_marked + 255) / 256)), dim3(256), 0,
                        s, mark_workspace, out_rows, marked, n_marked);
-  const int vb = vec_bytes(row_bytes, out, out);
+  const int vb = vec_bytes(row_bytes, row_bytes, row_bytes, out, out);
   const int64_t cpr = row_bytes / vb;
   const int tl = tpr_log2_for(cpr);
   dim3 grid;

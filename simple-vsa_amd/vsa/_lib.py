@@ -42,7 +42,8 @@ SIGNATURES = {
     "vsa_sparse_bwd_dkdv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                             _I64, _I32, _I32, _I32, _F, _I32, _P],
     "vsa_tile_metadata": [_I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P],
-    "vsa_rows_move": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _P],
+    "vsa_rows_move": [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P,
+                      _I64, _P],
     "vsa_rows_zero_unmarked": [_P, _I64, _I64, _I64, _P, _I64, _P, _P],
 }
 _RESTYPES = {"vsa_status_string": ctypes.c_char_p, "vsa_version": ctypes.c_char_p}

@@ -16,10 +16,20 @@ stream, with no device synchronisation.
 
 The building blocks (pooling, coarse attention + Top-K, CSR inversion, fine
 forward / backward) are exposed as functions so tests can check each kernel.
+
+The MFMA kernels exist for block volumes 64 / 128 / 256 and head dims 64 /
+128.  Other shapes the reference accepts on the GPU (volume in [1, 128],
+head_dim <= 128; triton_impl.py:379-384) run on the same kernels after a
+differentiable zero-padding of each block to the next kernel volume and of
+the head dim to the next kernel width (gfx950 row kernels); the softmax scale
+stays 1/sqrt(head_dim) of the caller's tensors.  Padded query rows are
+computed and dropped, padded keys are masked by the block sizes, padded
+channels are zero in every dot product.
 """
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import Optional, Tuple, Union
 
@@ -27,6 +37,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
+from .tiling import _move, _zero_unmarked
 
 SUPPORTED_BLOCKS = (64, 128, 256)
 SUPPORTED_HEAD_DIMS = (64, 128)
@@ -82,10 +93,102 @@ def _check_device_path(q, k, v, block_elements) -> None:
         raise ValueError("q, k, and v must have the same dtype")
     if q.dtype not in MFMA_DTYPES:
         raise ValueError("the MI355X kernels support float16 and bfloat16")
-    if block_elements not in SUPPORTED_BLOCKS:
-        raise ValueError(f"the MI355X kernels support block_size volumes {SUPPORTED_BLOCKS}")
-    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"the MI355X kernels support head_dim in {SUPPORTED_HEAD_DIMS}")
+    _kernel_block(block_elements)
+    _kernel_dim(q.shape[-1])
+
+
+def _kernel_block(be: int) -> int:
+    """Block volume the kernels run for a caller's volume ``be``."""
+    if be in SUPPORTED_BLOCKS:
+        return be
+    if not 1 <= be <= 128:
+        raise ValueError("the MI355X kernels support block_size volumes in [1, 128] or 256")
+    return 64 if be <= 64 else 128
+
+
+def _kernel_dim(d: int) -> int:
+    """Head dim the kernels run for a caller's head dim ``d``."""
+    if d in SUPPORTED_HEAD_DIMS:
+        return d
+    if not 1 <= d <= 128:
+        raise ValueError("the MI355X kernels support head_dim <= 128")
+    return 64 if d <= 64 else 128
+
+
+@functools.lru_cache(maxsize=32)
+def _block_rows(s: int, be: int, kbe: int, device: torch.device) -> Tensor:
+    """Row of token i in the layout padded from blocks of be to blocks of kbe."""
+    i = torch.arange(s, device=device, dtype=torch.long)
+    return torch.div(i, be, rounding_mode="floor") * kbe + i % be
+
+
+class _Pad(torch.autograd.Function):
+    """[B, H, S, d] -> [B, H, (S/be)*kbe, kd], zero rows and channels added."""
+
+    @staticmethod
+    def forward(ctx, x, rows, out_rows, kd):
+        x = x.contiguous()
+        b, h, s, d = x.shape
+        out = torch.empty((b, h, out_rows, kd), dtype=x.dtype, device=x.device)
+        xv, ov = x.view(b * h, s, d), out.view(b * h, out_rows, kd)
+        if out_rows != s:
+            _zero_unmarked(ov, rows)
+        _move(xv, ov, None, None, rows, None, s, copy_bytes=d * x.element_size())
+        ctx.save_for_backward(rows)
+        ctx.shape = (b, h, s, d)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (rows,) = ctx.saved_tensors
+        return _unpad(g, rows, ctx.shape), None, None, None
+
+
+def _unpad(x: Tensor, rows: Tensor, shape) -> Tensor:
+    b, h, s, d = shape
+    x = x.contiguous()
+    out = torch.empty(shape, dtype=x.dtype, device=x.device)
+    _move(x.view(b * h, x.shape[2], x.shape[3]), out.view(b * h, s, d), rows, None, None, None,
+          s, copy_bytes=d * x.element_size())
+    return out
+
+
+class _Unpad(torch.autograd.Function):
+    """Inverse of _Pad: keep the caller's rows and channels."""
+
+    @staticmethod
+    def forward(ctx, x, rows, shape):
+        ctx.save_for_backward(rows)
+        ctx.padded = (x.shape[2], x.shape[3])
+        return _unpad(x, rows, shape)
+
+    @staticmethod
+    def backward(ctx, g):
+        (rows,) = ctx.saved_tensors
+        return _Pad.apply(g, rows, *ctx.padded), None, None
+
+
+def _padded(q, k, be):
+    """(kbe, kd, pad_q, pad_k, unpad_out) for a shape without its own kernel,
+    or None when the kernels take the tensors as they are."""
+    d = q.shape[-1]
+    kbe, kd = _kernel_block(be), _kernel_dim(d)
+    if kbe == be and kd == d:
+        return None
+    rq = _block_rows(q.shape[2], be, kbe, q.device)
+    rk = _block_rows(k.shape[2], be, kbe, k.device)
+    nq, nk = q.shape[2] // be * kbe, k.shape[2] // be * kbe
+
+    def pad_q(x, width=kd):
+        return None if x is None else _Pad.apply(x, rq, nq, width)
+
+    def pad_k(x):
+        return _Pad.apply(x, rk, nk, kd)
+
+    def unpad_out(x):
+        return _Unpad.apply(x, rq, tuple(q.shape))
+
+    return kbe, kd, pad_q, pad_k, unpad_out
 
 
 def _i32(x: Tensor, device) -> Tensor:
@@ -279,6 +382,14 @@ def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
     _check_device_path(q, k, v, be)
     _validate_route(q, k, selected, variable_block_sizes, be)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    pads = _padded(q, k, be)
+    if pads is not None:
+        kbe, _, pad_q, pad_k, unpad_out = pads
+        with torch.cuda.device(q.device):
+            out = mi355x_sparse_attention(pad_q(q), pad_k(k), pad_k(v), selected,
+                                          variable_block_sizes, block_size=(1, 1, kbe),
+                                          sm_scale=scale)
+            return unpad_out(out)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     selected = _i32(selected, q.device)
     vbs = _i32(variable_block_sizes, q.device)
@@ -294,8 +405,7 @@ def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
 
 class _VSA(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, gate, vbs, qvbs, topk_, be):
-        scale = 1.0 / math.sqrt(q.shape[-1])
+    def forward(ctx, q, k, v, gate, vbs, qvbs, topk_, be, scale):
         qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
         _, probs, outc, sel = coarse_forward(qc, kc, vc, topk_, scale)
         out, lse = sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
@@ -312,7 +422,7 @@ class _VSA(torch.autograd.Function):
         dqc, dkc, dvc = coarse_backward(qc, kc, vc, probs, d_outc, ctx.scale)
         dq, dk, dv = sparse_backward(q, k, v, dout, lse, delta, sel, vbs, ctx.be, ctx.scale,
                                      dqc=dqc, dkc=dkc, dvc=dvc, q_variable_block_sizes=qvbs)
-        return dq, dk, dv, d_gate, None, None, None, None
+        return dq, dk, dv, d_gate, None, None, None, None, None
 
 
 def _prepare_gate(gate: Optional[Tensor], q: Tensor) -> Optional[Tensor]:
@@ -338,20 +448,31 @@ def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
     validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
     _check_device_path(q, k, v, be)
     gate = _prepare_gate(compress_attn_weight, q)
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    scale = 1.0 / math.sqrt(q.shape[-1])
     vbs = _i32(variable_block_sizes, q.device)
     qvbs = _i32(q_variable_block_sizes, q.device)
     with torch.cuda.device(q.device):
-        needs_grad = torch.is_grad_enabled() and (
-            q.requires_grad or k.requires_grad or v.requires_grad
-            or (gate is not None and gate.requires_grad))
-        if needs_grad:
-            return _VSA.apply(q, k, v, gate, vbs, qvbs, topk, be)
-        scale = 1.0 / math.sqrt(q.shape[-1])
-        qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
-        _, _, outc, sel = coarse_forward(qc, kc, vc, topk, scale)
-        return sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
-                              want_lse=False)[0]
+        pads = _padded(q, k, be)
+        if pads is not None:
+            kbe, kd, pad_q, pad_k, unpad_out = pads
+            gate = pad_q(gate, kd if gate is not None and gate.shape[-1] == q.shape[-1] else 1)
+            return unpad_out(_vsa(pad_q(q), pad_k(k), pad_k(v), gate, vbs, qvbs, topk, kbe,
+                                  scale))
+        return _vsa(q.contiguous(), k.contiguous(), v.contiguous(), gate, vbs, qvbs, topk, be,
+                    scale)
+
+
+def _vsa(q, k, v, gate, vbs, qvbs, topk, be, scale):
+    """The op on kernel-native shapes (contiguous, be and head dim supported)."""
+    needs_grad = torch.is_grad_enabled() and (
+        q.requires_grad or k.requires_grad or v.requires_grad
+        or (gate is not None and gate.requires_grad))
+    if needs_grad:
+        return _VSA.apply(q, k, v, gate, vbs, qvbs, topk, be, scale)
+    qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
+    _, _, outc, sel = coarse_forward(qc, kc, vc, topk, scale)
+    return sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
+                          want_lse=False)[0]
 
 
 def mi355x_route(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, block_size=64):
@@ -359,7 +480,16 @@ def mi355x_route(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, bl
     as fp32 holding input-dtype values.  For inspection and parity tests."""
     be = as_block_elements(block_size)
     validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
-    qc, kc, vc = block_mean_qkv(q.contiguous(), k.contiguous(), v.contiguous(),
-                                variable_block_sizes, q_variable_block_sizes, be)
-    scores, _, _, sel = coarse_forward(qc, kc, vc, topk, 1.0 / math.sqrt(q.shape[-1]))
+    _check_device_path(q, k, v, be)
+    scale = 1.0 / math.sqrt(q.shape[-1])
+    vbs = _i32(variable_block_sizes, q.device)
+    qvbs = _i32(q_variable_block_sizes, q.device)
+    with torch.cuda.device(q.device), torch.no_grad():
+        pads = _padded(q, k, be)
+        if pads is not None:
+            be, _, pad_q, pad_k, _ = pads
+            q, k, v = pad_q(q), pad_k(k), pad_k(v)
+        qc, kc, vc = block_mean_qkv(q.contiguous(), k.contiguous(), v.contiguous(), vbs, qvbs,
+                                    be)
+        scores, _, _, sel = coarse_forward(qc, kc, vc, topk, scale)
     return scores, sel

@@ -95,10 +95,14 @@ def _rows(x: Tensor) -> Tuple[int, int, int]:
 
 
 def _move(x: Tensor, out: Tensor, src: Optional[Tensor], src_outer: Optional[Tensor],
-          dst: Optional[Tensor], dst_outer: Optional[Tensor], n: int) -> None:
-    B, xr, row = _rows(x)
-    _, orow, _ = _rows(out)
-    _lib.call("vsa_rows_move", _lib.ptr(x), xr, _lib.ptr(out), orow, B, row,
+          dst: Optional[Tensor], dst_outer: Optional[Tensor], n: int,
+          copy_bytes: Optional[int] = None) -> None:
+    """out[b, d(i)] = x[b, s(i)] for i < n (rows along dim 1); with copy_bytes,
+    only that prefix of each row is copied and the rest of the out row zeroed."""
+    B, xr, xrow = _rows(x)
+    _, orow, orb = _rows(out)
+    cb = min(xrow, orb) if copy_bytes is None else copy_bytes
+    _lib.call("vsa_rows_move", _lib.ptr(x), xr, xrow, _lib.ptr(out), orow, orb, cb, B,
               _lib.ptr(src), src.numel() if src is not None else 0, _lib.ptr(src_outer),
               _lib.ptr(dst), dst.numel() if dst is not None else 0, _lib.ptr(dst_outer), n,
               _lib.stream_of(x))

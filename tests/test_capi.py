@@ -65,8 +65,12 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     # tiling entry points validate before launching
     assert lib.vsa_tile_metadata(0, 4, 4, 2, 2, 2, p, p, p, p, None) == -2
     assert lib.vsa_tile_metadata(4, 4, 4, 2, 2, 2, None, p, p, p, None) == -1
-    assert lib.vsa_rows_move(None, 4, p, 4, 1, 16, None, 0, None, None, 0, None, 4, None) == -1
-    assert lib.vsa_rows_move(p, 4, p, 4, 1, 0, None, 0, None, None, 0, None, 4, None) == -2
+    assert lib.vsa_rows_move(None, 4, 16, p, 4, 16, 16, 1, None, 0, None, None, 0, None, 4,
+                             None) == -1
+    assert lib.vsa_rows_move(p, 4, 16, p, 4, 16, 0, 1, None, 0, None, None, 0, None, 4,
+                             None) == -2
+    assert lib.vsa_rows_move(p, 4, 16, p, 4, 8, 16, 1, None, 0, None, None, 0, None, 4,
+                             None) == -2     # copy longer than the destination row
     assert lib.vsa_rows_zero_unmarked(p, 4, 1, 16, None, 2, p, None) == -1
 
 
@@ -101,3 +105,16 @@ def test_block_volume_and_gate_shape_helpers():
     assert M._prepare_gate(torch.ones(1, 2, 16, 1), q).shape == (1, 2, 16, 1)
     with pytest.raises(ValueError, match="compress_attn_weight"):
         M._prepare_gate(torch.ones(1, 2, 16, 4), q)
+
+
+def test_kernel_shape_mapping_and_limits():
+    # shapes the reference's GPU path accepts map onto kernel shapes; others raise
+    assert M._kernel_block(256) == 256 and M._kernel_block(64) == 64
+    assert M._kernel_block(27) == 64 and M._kernel_block(100) == 128 and M._kernel_block(1) == 64
+    assert M._kernel_dim(80) == 128 and M._kernel_dim(32) == 64 and M._kernel_dim(128) == 128
+    with pytest.raises(ValueError, match=r"\[1, 128\] or 256"):
+        M._kernel_block(200)
+    with pytest.raises(ValueError, match="head_dim"):
+        M._kernel_dim(256)
+    rows = M._block_rows(12, 3, 64, torch.device("cpu"))
+    assert rows.tolist() == [0, 1, 2, 64, 65, 66, 128, 129, 130, 192, 193, 194]
