@@ -42,6 +42,10 @@ WORKLOADS = {
                block=(1, 1, 256), topk=45, gate=None, every8th=192, amp=0.5),
     "c5": dict(name="Route-skew explicit routing (BASELINE configs[4])", B=1, H=24, S=40960,
                D=64, block=(1, 1, 64), topk=32, gate=None, zipf=1.2),
+    # not a BASELINE row: the c3 sequence in FastVideo's native (4,4,4) tiles at the same
+    # 87.5 % sparsity (64-token blocks, topk 80)
+    "t444": dict(name="c3 sequence with FastVideo (4,4,4) tiles", B=1, H=40, S=40960, D=128,
+                 block=(4, 4, 4), topk=80, gate="full"),
 }
 
 

@@ -2,6 +2,7 @@
 // padded block mean, coarse block attention + Top-K routing, CSR inverse
 // routing, backward preprocessing (delta + combine gradients) and the coarse
 // branch backward.  The MFMA fine kernels live in fine_fwd.hip / fine_bwd.hip.
+#include "coarse.h"
 #include "vsa_device.h"
 #include "vsa_launch.h"
 
@@ -59,69 +60,21 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Top-K by rank: element j is selected iff fewer than `topk` elements beat it,
-// where i beats j when s_i > s_j, or s_i == s_j and i < j.  Scores are compared
-// through a total-order integer key (-0 == +0; NaN above +inf, as torch.topk
-// ranks it), so the ranks are a permutation and exactly `topk` ids are chosen.
-// Selected ids are written in ascending id order.  `row` lives in LDS; `scan`
-// holds 256 ints.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int order_key(float x) {
-  uint32_t u = __float_as_uint(x + 0.0f);  // folds -0 into +0
-  if (x != x) u = 0x7fffffffu;             // NaN: larger than +inf
-  return (int)u >= 0 ? (int)u : (int)(u ^ 0x7fffffffu);
-}
+constexpr int kMaxCoarseBlocks = 4096;  // generic kernels keep [2 Kb + D] fp32 rows in LDS
 
-__device__ void topk_row(const float* row, int kb, int topk, int32_t* __restrict__ dst,
-                         int* scan) {
-  const int per = (kb + 255) / 256;
-  const int j0 = threadIdx.x * per;
-  unsigned flags = 0;  // bit m set: element j0+m selected (per <= 32)
-  int nsel = 0;
-  for (int m = 0; m < per; ++m) {
-    const int j = j0 + m;
-    if (j >= kb) break;
-    const int sj = order_key(row[j]);
-    int rank = 0;
-    for (int i = 0; i < kb; ++i) {
-      const int si = order_key(row[i]);
-      rank += (si > sj) || (si == sj && i < j);
-    }
-    if (rank < topk) {
-      flags |= 1u << m;
-      ++nsel;
-    }
-  }
-  // exclusive scan of nsel over the block (Hillis-Steele in LDS)
-  scan[threadIdx.x] = nsel;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {
-    int add = threadIdx.x >= o ? scan[threadIdx.x - o] : 0;
-    __syncthreads();
-    scan[threadIdx.x] += add;
-    __syncthreads();
-  }
-  int pos = scan[threadIdx.x] - nsel;
-  for (int m = 0; m < per; ++m)
-    if ((flags & (1u << m)) && pos < topk) dst[pos++] = j0 + m;
-}
-
-constexpr int kMaxCoarseBlocks = 4096;  // keeps dynamic LDS under 64 KiB
-
-// One workgroup per (bh, query block): scores in T, softmax in T, out_c in T,
-// then Top-K on the scores row (common.py:159-166, triton_impl.py:1710).
+// Generic coarse forward (fp32, or head dims the MFMA kernels do not take):
+// one workgroup per (bh, query block); scores in T, softmax in T, out_c in T
+// (common.py:159-166).  The Top-K route runs afterwards (topk_radix).
 template <typename T>
 __global__ __launch_bounds__(256) void coarse_fwd_kernel(
     const T* __restrict__ qc, const T* __restrict__ kc, const T* __restrict__ vc,
-    float* __restrict__ scores, float* __restrict__ probs, T* __restrict__ outc,
-    int32_t* __restrict__ selected, int qb, int kb, int D, int topk, float scale) {
+    float* __restrict__ scores, float* __restrict__ probs, T* __restrict__ outc, int qb, int kb,
+    int D, float scale) {
   extern __shared__ float smem[];
   float* qrow = smem;            // D
   float* srow = qrow + D;        // kb
   float* prow = srow + kb;       // kb
   float* red = prow + kb;        // 4
-  int* scan = reinterpret_cast<int*>(red + 4);  // 256
   const int64_t b = blockIdx.y;
   const int i = blockIdx.x;
   const T* qsrc = qc + (b * qb + i) * D;
@@ -159,19 +112,6 @@ __global__ __launch_bounds__(256) void coarse_fwd_kernel(
     for (int j = 0; j < kb; ++j) acc = fmaf(prow[j], Elem<T>::to_f(vbase[(int64_t)j * D + d]), acc);
     outc[(b * qb + i) * D + d] = Elem<T>::from_f(acc);
   }
-  if (selected != nullptr) topk_row(srow, kb, topk, selected + (b * qb + i) * (int64_t)topk, scan);
-}
-
-__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ scores,
-                                                    int32_t* __restrict__ selected, int kb,
-                                                    int topk) {
-  extern __shared__ float smem[];
-  float* row = smem;
-  int* scan = reinterpret_cast<int*>(row + kb);
-  const int64_t r = blockIdx.x;
-  for (int j = threadIdx.x; j < kb; j += 256) row[j] = scores[r * kb + j];
-  __syncthreads();
-  topk_row(row, kb, topk, selected + r * topk, scan);
 }
 
 // ---------------------------------------------------------------------------
@@ -465,24 +405,29 @@ extern "C" int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
   if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   if (selected && (topk < 1 || topk > kb)) return VSA_ERR_SHAPE;
-  const size_t shm = (size_t)(D + 2 * kb + 4) * sizeof(float) + 256 * sizeof(int);
   hipStream_t s = (hipStream_t)stream;
+  if (coarse_mfma_supported(D, dtype)) {
+    const int rc = coarse_fwd_mfma(q_c, k_c, v_c, scores, probs, out_c, bh, qb, kb, D, scale,
+                                   dtype, s);
+    if (rc || !selected) return rc;
+    return topk_radix(scores, selected, bh * qb, kb, topk, s);
+  }
+  const size_t shm = (size_t)(D + 2 * kb + 4) * sizeof(float);
   VSA_DISPATCH_ALL(dtype, T, {
     hipLaunchKernelGGL(coarse_fwd_kernel<T>, dim3(qb, (unsigned)bh), dim3(256), shm, s,
-                       (const T*)q_c, (const T*)k_c, (const T*)v_c, scores, probs, (T*)out_c,
-                       selected, qb, kb, D, topk, scale);
+                       (const T*)q_c, (const T*)k_c, (const T*)v_c, scores, probs, (T*)out_c, qb,
+                       kb, D, scale);
   });
-  return vsa_check_launch();
+  const int rc = vsa_check_launch();
+  if (rc || !selected) return rc;
+  return topk_radix(scores, selected, bh * qb, kb, topk, s);
 }
 
 extern "C" int vsa_topk(const float* scores, int32_t* selected, int64_t rows, int32_t kb,
                         int32_t topk, void* stream) {
   if (!scores || !selected) return VSA_ERR_NULL;
   if (rows <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || topk < 1 || topk > kb) return VSA_ERR_SHAPE;
-  const size_t shm = (size_t)kb * sizeof(float) + 256 * sizeof(int);
-  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(256), shm, (hipStream_t)stream,
-                     scores, selected, kb, topk);
-  return vsa_check_launch();
+  return topk_radix(scores, selected, rows, kb, topk, (hipStream_t)stream);
 }
 
 constexpr int kMaxCsrBlocks = 8064;  // 2*Kb + 256 ints of LDS stay under 64 KiB
@@ -535,6 +480,9 @@ extern "C" int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c,
   if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+  if (coarse_mfma_supported(D, dtype))
+    return coarse_bwd_mfma(q_c, k_c, v_c, probs, d_out_c, ds, d_q_c, d_k_c, d_v_c, bh, qb, kb, D,
+                           scale, dtype, s);
   const size_t shm = (size_t)(D + kb + 4) * sizeof(float);
   int rc = 0;
   VSA_DISPATCH_ALL(dtype, T, {

@@ -81,6 +81,14 @@ __device__ __forceinline__ typename Elem<T>::vec8 as_vec8(u32x4 x) {
   return __builtin_bit_cast(typename Elem<T>::vec8, x);
 }
 
+// Total-order integer key of a score: larger score -> larger key; -0 == +0;
+// NaN above +inf (torch.topk's ranking).
+__device__ __forceinline__ int order_key(float x) {
+  uint32_t u = __float_as_uint(x + 0.0f);  // folds -0 into +0
+  if (x != x) u = 0x7fffffffu;             // NaN: larger than +inf
+  return (int)u >= 0 ? (int)u : (int)(u ^ 0x7fffffffu);
+}
+
 // ---------------------------------------------------------------------------
 // Swizzled row-major LDS tiles.
 //
