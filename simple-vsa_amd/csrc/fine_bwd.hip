@@ -8,7 +8,7 @@
 // in a separate block-mean backward (fused_common.py:62-103) and autograd adds
 // the two gradients afterwards.
 //
-// dQ, per wave (32 queries) and 64-key chunk, P recomputed from the saved LSE:
+// dQ, per wave (32 queries) and KC-key chunk, P recomputed from the saved LSE:
 //   S^T  = K Q^T,  dP^T = V dO^T,  dS^T = P^T (dP^T - delta),  dQ^T += K^T dS^T
 // dK/dV, per wave (32 keys) and 32-query sub-tile of an in-edge query block:
 //   S = Q K^T,  dP = dO V^T,  dS = P (dP - delta),  dV^T += dO^T P,  dK^T += Q^T dS
@@ -27,12 +27,15 @@ struct DqCfg {
   static constexpr int QT = BE >= 128 ? 128 : BE;
   static constexpr int NW = QT / 32;
   static constexpr int NT = NW * 64;
-  static constexpr int KC = 64;
+  // keys per chunk: 32 for (D 128, block 64), so that a 2-wave workgroup's
+  // double buffer is 32 KiB and four workgroups share a CU
+  static constexpr int KC = (D == 128 && BE == 64) ? 32 : 64;
+  static constexpr int NSM = KC / 32;            // 32-key sub-tiles per chunk
   static constexpr int TILE = KC * D;            // one K (or V) chunk, swizzled row-major
   static constexpr int STAGE = 2 * TILE;
 };
 
-template <int BE>
+template <int BE, int KC>
 __device__ __forceinline__ bool next_valid_chunk_b(const int32_t* __restrict__ sel,
                                                    const int32_t* __restrict__ vbs, int topk,
                                                    int kb, int& s, int& c, int& kv, int& nvb) {
@@ -42,7 +45,7 @@ __device__ __forceinline__ bool next_valid_chunk_b(const int32_t* __restrict__ s
     kv = __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(s)]);
     if (kv >= 0 && kv < kb) {
       nvb = __builtin_amdgcn_readfirstlane(clamp_valid(vbs[kv], BE));
-      if (c * 64 < nvb) return true;
+      if (c * KC < nvb) return true;
     }
     ++s;
     c = 0;
@@ -93,11 +96,13 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   const T* kbase = k + (int64_t)b * skv * D;
   const T* vbase = v + (int64_t)b * skv * D;
 
+  TileDma<T, D, C::KC, C::NT> tdma;
+  tdma.init();
   auto dma = [&](int kvb, int ch, int stg) {
     const int64_t off = ((int64_t)kvb * BE + ch * C::KC) * D;
     T* Ks = smem + stg * C::STAGE;
-    dma_tile<T, D, C::KC, C::NT>(Ks, kbase + off);
-    dma_tile<T, D, C::KC, C::NT>(Ks + C::TILE, vbase + off);
+    tdma.copy(Ks, kbase + off);
+    tdma.copy(Ks + C::TILE, vbase + off);
   };
 
   f32x16 dqacc[D / 32];
@@ -105,39 +110,40 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   for (int mt = 0; mt < D / 32; ++mt) dqacc[mt] = f32x16{};
 
   int s = 0, ch = 0, kv = 0, nvb = 0;
-  bool have = next_valid_chunk_b<BE>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
+  bool have = next_valid_chunk_b<BE, C::KC>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
   if (have) dma(kv, ch, 0);
   dma_wait();
   __syncthreads();
   int stage = 0;
   while (have) {
-    const int nv = min(nvb - ch * 64, 64);
+    const int nv = min(nvb - ch * C::KC, C::KC);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
-    const bool have2 = next_valid_chunk_b<BE>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
+    const bool have2 = next_valid_chunk_b<BE, C::KC>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
     if (have2) dma(kv2, ch2, stage ^ 1);
     const T* Ks = smem + stage * C::STAGE;
     const T* Vs = Ks + C::TILE;
 
-    f32x16 sacc[2] = {f32x16{}, f32x16{}};
-    f32x16 pacc[2] = {f32x16{}, f32x16{}};
+    f32x16 sacc[C::NSM], pacc[C::NSM];
+#pragma unroll
+    for (int smt = 0; smt < C::NSM; ++smt) sacc[smt] = pacc[smt] = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
-      for (int smt = 0; smt < 2; ++smt) {
+      for (int smt = 0; smt < C::NSM; ++smt) {
         sacc[smt] = E::mfma32(row_a8<T, D>(Ks, smt * 32 + r, ks, h), qf[ks], sacc[smt]);
         pacc[smt] = E::mfma32(row_a8<T, D>(Vs, smt * 32 + r, ks, h), df[ks], pacc[smt]);
       }
     }
     // dS^T = P^T (dP^T - delta), consumed 8 keys at a time as the B operand
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < 2 * C::NSM; ++kk) {
       float dsv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int i = 8 * (kk & 1) + e;
         const float p = fast_exp2(fmaf(sacc[kk >> 1][i], c2, -my_lse));
         dsv[e] = p * (pacc[kk >> 1][i] - my_delta);
-        if (nv < 64) {
+        if (nv < C::KC) {
           const int key = (kk >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
           if (key >= nv) dsv[e] = 0.f;
         }

@@ -5,16 +5,17 @@
 //
 // Work decomposition: one workgroup owns QT query rows of one (b, h) (QT = 128
 // for block volume >= 128, else the block), one wave owns 32 of them.  The
-// workgroup walks the selected KV blocks of its query block in 64-key chunks;
+// workgroup walks the selected KV blocks of its query block in KC-key chunks
+// (64 keys; 32 for head_dim 128 with 64-token blocks);
 // every chunk is copied once into LDS (direct global->LDS loads) as two
 // swizzled row-major tiles (K and V) shared by all waves; the next chunk's
 // copy is in flight while the current chunk is multiplied (double-buffered
 // LDS, one barrier per chunk).
 //
 // Per wave and chunk:
-//   S^T (64 x 32)  = K (64 x D) . Q^T (D x 32)           A = K from LDS, B = Q in VGPRs
+//   S^T (KC x 32)  = K (KC x D) . Q^T (D x 32)           A = K from LDS, B = Q in VGPRs
 //   online softmax per query (each lane owns one query: column r of S^T)
-//   O^T (D x 32)  += V^T (D x 64) . P^T (64 x 32)        A = V^T by transpose reads, B = P
+//   O^T (D x 32)  += V^T (D x KC) . P^T (KC x 32)        A = V^T by transpose reads, B = P
 // Holding S and O transposed keeps the softmax statistics and the O rescale
 // lane-local; only the row max crosses the two lane halves.  The running max
 // is only moved when a chunk exceeds it by more than 2^kRescaleSlack (the
@@ -30,7 +31,10 @@ struct FwdCfg {
   static constexpr int QT = BE >= 128 ? 128 : BE;  // queries per workgroup
   static constexpr int NW = QT / 32;               // waves per workgroup
   static constexpr int NT = NW * 64;
-  static constexpr int KC = 64;                    // keys per chunk
+  // keys per chunk: 32 for (D 128, block 64) so that a 2-wave workgroup's
+  // double buffer is 32 KiB and four workgroups share a CU
+  static constexpr int KC = (D == 128 && BE == 64) ? 32 : 64;
+  static constexpr int NSM = KC / 32;              // 32-key sub-tiles per chunk
   static constexpr int TILE = KC * D;              // elements of one K (or V) chunk
   static constexpr int STAGE = 2 * TILE;           // K and V
 };
@@ -38,7 +42,7 @@ struct FwdCfg {
 constexpr float kRescaleSlack = 8.0f;  // log2 units
 
 // Advance (slot, chunk) to the next chunk that holds at least one valid key.
-template <int BE>
+template <int BE, int KC>
 __device__ __forceinline__ bool next_valid_chunk(const int32_t* __restrict__ sel,
                                                  const int32_t* __restrict__ vbs, int topk,
                                                  int kb, int& s, int& c, int& kv, int& nvb) {
@@ -48,7 +52,7 @@ __device__ __forceinline__ bool next_valid_chunk(const int32_t* __restrict__ sel
     kv = __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(s)]);
     if (kv >= 0 && kv < kb) {
       nvb = __builtin_amdgcn_readfirstlane(clamp_valid(vbs[kv], BE));
-      if (c * 64 < nvb) return true;
+      if (c * KC < nvb) return true;
     }
     ++s;
     c = 0;
@@ -93,11 +97,13 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   const T* kbase = k + (int64_t)b * skv * D;
   const T* vbase = v + (int64_t)b * skv * D;
 
+  TileDma<T, D, C::KC, C::NT> tdma;
+  tdma.init();
   auto dma = [&](int kvb, int ch, int stg) {
     const int64_t off = ((int64_t)kvb * BE + ch * C::KC) * D;
     T* Ks = smem + stg * C::STAGE;
-    dma_tile<T, D, C::KC, C::NT>(Ks, kbase + off);
-    dma_tile<T, D, C::KC, C::NT>(Ks + C::TILE, vbase + off);
+    tdma.copy(Ks, kbase + off);
+    tdma.copy(Ks + C::TILE, vbase + off);
   };
 
   float m = -INFINITY;  // running max in log2 units (scaled)
@@ -107,31 +113,33 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   for (int mt = 0; mt < D / 32; ++mt) oacc[mt] = f32x16{};
 
   int s = 0, ch = 0, kv = 0, nvb = 0;
-  bool have = next_valid_chunk<BE>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
+  bool have = next_valid_chunk<BE, C::KC>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
   if (have) dma(kv, ch, 0);
   dma_wait();
   __syncthreads();
   int stage = 0;
   while (have) {
-    const int nv = min(nvb - ch * 64, 64);
+    const int nv = min(nvb - ch * C::KC, C::KC);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
-    const bool have2 = next_valid_chunk<BE>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
+    const bool have2 = next_valid_chunk<BE, C::KC>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
     if (have2) dma(kv2, ch2, stage ^ 1);  // lands while this chunk is multiplied
 
     const T* Ks = smem + stage * C::STAGE;
     const T* Vs = Ks + C::TILE;
     // ---- S^T = K Q^T -------------------------------------------------------
-    f32x16 sacc[2] = {f32x16{}, f32x16{}};
+    f32x16 sacc[C::NSM];
+#pragma unroll
+    for (int smt = 0; smt < C::NSM; ++smt) sacc[smt] = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
-      for (int smt = 0; smt < 2; ++smt)
+      for (int smt = 0; smt < C::NSM; ++smt)
         sacc[smt] = E::mfma32(row_a8<T, D>(Ks, smt * 32 + r, ks, h), qf[ks], sacc[smt]);
     }
     // ---- online softmax (base 2, lazily rescaled) ---------------------------
-    if (nv < 64) {
+    if (nv < C::KC) {
 #pragma unroll
-      for (int smt = 0; smt < 2; ++smt)
+      for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
@@ -140,7 +148,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     }
     float smax = sacc[0][0];
 #pragma unroll
-    for (int smt = 0; smt < 2; ++smt)
+    for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) smax = fmaxf(smax, sacc[smt][i]);
     smax = fmaxf(smax, __shfl_xor(smax, 32, 64)) * c2;
@@ -152,15 +160,15 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
       for (int mt = 0; mt < D / 32; ++mt) oacc[mt] *= alpha;
       m = mnew;
     }
-    float p[2][16];
+    float p[C::NSM][16];
     const float negm = -m;
 #pragma unroll
-    for (int smt = 0; smt < 2; ++smt)
+    for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) p[smt][i] = fast_exp2(fmaf(sacc[smt][i], c2, negm));
-    if (nv < 64) {
+    if (nv < C::KC) {
 #pragma unroll
-      for (int smt = 0; smt < 2; ++smt)
+      for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
@@ -168,12 +176,12 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
         }
     }
 #pragma unroll
-    for (int smt = 0; smt < 2; ++smt)
+    for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) lsum += p[smt][i];
     // ---- O^T += V^T P^T ------------------------------------------------------
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < 2 * C::NSM; ++kk) {
       const V8 bop = pack8<T>(&p[kk >> 1][8 * (kk & 1)]);
 #pragma unroll
       for (int mt = 0; mt < D / 32; ++mt)

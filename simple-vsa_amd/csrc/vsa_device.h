@@ -243,6 +243,34 @@ __device__ __forceinline__ void dma_tile(T* dst, const T* __restrict__ src) {
   }
 }
 
+// dma_tile with the scalar-base form: the lane offsets of a NROWS x D tile are
+// computed once (they do not depend on which tile is copied) and every copy
+// passes only the wave-uniform global base, so no 64-bit per-lane addresses
+// stay live across a loop.
+template <typename T, int D, int NROWS, int NT>
+struct TileDma {
+  static constexpr int N = NROWS * D / 8 / NT;
+  static_assert(NROWS * D / 8 % NT == 0, "tile must split evenly over the workgroup");
+  uint32_t voff[N];  // byte offset of this lane's source chunk within the tile
+
+  __device__ __forceinline__ void init() {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      int c;
+      const int row = unswz_row_chunk<D>((i * (NT / 64) + wave) * 64 + lane, c);
+      voff[i] = opaque((uint32_t)((row * D + c * 8) * sizeof(T)));
+    }
+  }
+  // `src` and `dst` are wave-uniform
+  __device__ __forceinline__ void copy(T* dst, const T* src) const {
+    const uint32_t base =
+        __builtin_amdgcn_readfirstlane(lds_addr(dst) + (uint32_t)(threadIdx.x >> 6) * 1024u);
+#pragma unroll
+    for (int i = 0; i < N; ++i) dma16_s(voff[i], src, base + (uint32_t)i * (NT / 64) * 1024u);
+  }
+};
+
 // Wait until at most N of this wave's vector-memory loads are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
