@@ -35,24 +35,6 @@ struct DqCfg {
   static constexpr int STAGE = 2 * TILE;
 };
 
-template <int BE, int KC>
-__device__ __forceinline__ bool next_valid_chunk_b(const int32_t* __restrict__ sel,
-                                                   const int32_t* __restrict__ vbs, int topk,
-                                                   int kb, int& s, int& c, int& kv, int& nvb) {
-  // Uniform indices keep these reads on the scalar path: a vector load here
-  // would need vmcnt(0) and so wait for every K/V copy still in flight.
-  while (s < topk) {
-    kv = __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(s)]);
-    if (kv >= 0 && kv < kb) {
-      nvb = __builtin_amdgcn_readfirstlane(clamp_valid(vbs[kv], BE));
-      if (c * KC < nvb) return true;
-    }
-    ++s;
-    c = 0;
-  }
-  return false;
-}
-
 template <typename T, int D, int BE>
 __global__ __launch_bounds__((DqCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void
 sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -109,8 +91,10 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) dqacc[mt] = f32x16{};
 
+  RouteRegs<BE, C::KC> route{sel, kv_vbs, topk, kb};
+  route.load(0);
   int s = 0, ch = 0, kv = 0, nvb = 0;
-  bool have = next_valid_chunk_b<BE, C::KC>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
+  bool have = route.next(s, ch, kv, nvb);
   if (have) dma(kv, ch, 0);
   dma_wait();
   __syncthreads();
@@ -118,7 +102,7 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   while (have) {
     const int nv = min(nvb - ch * C::KC, C::KC);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
-    const bool have2 = next_valid_chunk_b<BE, C::KC>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
+    const bool have2 = route.next(s2, ch2, kv2, nvb2);
     if (have2) dma(kv2, ch2, stage ^ 1);
     const T* Ks = smem + stage * C::STAGE;
     const T* Vs = Ks + C::TILE;
@@ -143,7 +127,12 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
         const int i = 8 * (kk & 1) + e;
         const float p = fast_exp2(fmaf(sacc[kk >> 1][i], c2, -my_lse));
         dsv[e] = p * (pacc[kk >> 1][i] - my_delta);
-        if (nv < C::KC) {
+      }
+      if (nv < C::KC) {
+        keep_branch();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 8 * (kk & 1) + e;
           const int key = (kk >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
           if (key >= nv) dsv[e] = 0.f;
         }

@@ -41,23 +41,69 @@ struct FwdCfg {
 
 constexpr float kRescaleSlack = 8.0f;  // log2 units
 
-// Advance (slot, chunk) to the next chunk that holds at least one valid key.
-template <int BE, int KC>
-__device__ __forceinline__ bool next_valid_chunk(const int32_t* __restrict__ sel,
-                                                 const int32_t* __restrict__ vbs, int topk,
-                                                 int kb, int& s, int& c, int& kv, int& nvb) {
-  // Uniform indices keep these reads on the scalar path: a vector load here
-  // would need vmcnt(0) and so wait for every K/V copy still in flight.
-  while (s < topk) {
-    kv = __builtin_amdgcn_readfirstlane(sel[__builtin_amdgcn_readfirstlane(s)]);
-    if (kv >= 0 && kv < kb) {
-      nvb = __builtin_amdgcn_readfirstlane(clamp_valid(vbs[kv], BE));
-      if (c * KC < nvb) return true;
-    }
-    ++s;
-    c = 0;
+// Normalise, fused combine, store, LSE (one lane = one query row, holding
+// O^T column r and a partial row sum).
+template <typename T, int D>
+__device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float lsum, float m,
+                                             int64_t b, int myq, int qblk, int h, int sq, int qb,
+                                             T* __restrict__ out, float* __restrict__ lse,
+                                             const T* __restrict__ outc,
+                                             const T* __restrict__ gate, int gate_mode,
+                                             int gate_heads) {
+  using E = Elem<T>;
+  const float ltot = pair_sum32(lsum);
+  const float inv = 1.0f / ltot;
+  const int64_t tok = (int64_t)b * sq + myq;
+  if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
+  const T* ocrow = outc ? outc + ((int64_t)b * qb + qblk) * D : nullptr;
+  float gtok = 1.f;
+  if (outc && gate_mode == 2) gtok = E::to_f(gate[tok]);
+  // gate row of this token: [BH, Sq, D] (mode 1) or token-major [B, Sq, H, D] (mode 3)
+  const T* grow = nullptr;
+  if (gate_mode == 1) grow = gate + tok * D;
+  if (gate_mode == 3)
+    grow = gate + (((int64_t)(b / gate_heads) * sq + myq) * gate_heads + b % gate_heads) * D;
+  // the combine operands are loaded together, so their latency is paid once
+  u32x2 ocr[D / 32][4], gr[D / 32][4];
+  if (ocrow) {
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        ocr[mt][g] = *reinterpret_cast<const u32x2*>(ocrow + mt * 32 + 8 * g + 4 * h);
   }
-  return false;
+  if (grow) {
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        gr[mt][g] = *reinterpret_cast<const u32x2*>(grow + mt * 32 + 8 * g + 4 * h);
+  }
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = mt * 32 + 8 * g + 4 * h;
+      float val[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) val[e] = oacc[mt][4 * g + e] * inv;
+      if (ocrow) {
+        const T* oc = reinterpret_cast<const T*>(&ocr[mt][g]);
+        float gv[4] = {gtok, gtok, gtok, gtok};
+        if (grow) {
+          const T* gg = reinterpret_cast<const T*>(&gr[mt][g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) gv[e] = E::to_f(gg[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = fmaf(E::to_f(oc[e]), gv[e], val[e]);
+      }
+      T o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = E::from_f(val[e]);
+      *reinterpret_cast<u32x2*>(out + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
+    }
+  }
 }
 
 template <typename T, int D, int BE>
@@ -112,8 +158,10 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) oacc[mt] = f32x16{};
 
+  RouteRegs<BE, C::KC> route{sel, kv_vbs, topk, kb};
+  route.load(0);
   int s = 0, ch = 0, kv = 0, nvb = 0;
-  bool have = next_valid_chunk<BE, C::KC>(sel, kv_vbs, topk, kb, s, ch, kv, nvb);
+  bool have = route.next(s, ch, kv, nvb);
   if (have) dma(kv, ch, 0);
   dma_wait();
   __syncthreads();
@@ -121,7 +169,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   while (have) {
     const int nv = min(nvb - ch * C::KC, C::KC);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
-    const bool have2 = next_valid_chunk<BE, C::KC>(sel, kv_vbs, topk, kb, s2, ch2, kv2, nvb2);
+    const bool have2 = route.next(s2, ch2, kv2, nvb2);
     if (have2) dma(kv2, ch2, stage ^ 1);  // lands while this chunk is multiplied
 
     const T* Ks = smem + stage * C::STAGE;
@@ -138,6 +186,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     }
     // ---- online softmax (base 2, lazily rescaled) ---------------------------
     if (nv < C::KC) {
+      keep_branch();
 #pragma unroll
       for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
@@ -146,12 +195,13 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
           if (key >= nv) sacc[smt][i] = -INFINITY;
         }
     }
-    float smax = sacc[0][0];
+    float m4[4] = {sacc[0][0], sacc[0][1], sacc[0][2], sacc[0][3]};  // short chains
 #pragma unroll
     for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) smax = fmaxf(smax, sacc[smt][i]);
-    smax = fmaxf(smax, __shfl_xor(smax, 32, 64)) * c2;
+      for (int i = 0; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], sacc[smt][i]);
+    float smax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+    smax = pair_max32(smax) * c2;
     if (__any(smax > m + kRescaleSlack)) {
       const float mnew = fmaxf(m, smax);
       const float alpha = fast_exp2(m - mnew);
@@ -167,6 +217,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 #pragma unroll
       for (int i = 0; i < 16; ++i) p[smt][i] = fast_exp2(fmaf(sacc[smt][i], c2, negm));
     if (nv < C::KC) {
+      keep_branch();
 #pragma unroll
       for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
@@ -175,10 +226,12 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
           if (key >= nv) p[smt][i] = 0.f;
         }
     }
+    float l4[4] = {0.f, 0.f, 0.f, 0.f};  // chunk row sum in four short chains
 #pragma unroll
     for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) lsum += p[smt][i];
+      for (int i = 0; i < 16; ++i) l4[i & 3] += p[smt][i];
+    lsum += (l4[0] + l4[1]) + (l4[2] + l4[3]);
     // ---- O^T += V^T P^T ------------------------------------------------------
 #pragma unroll
     for (int kk = 0; kk < 2 * C::NSM; ++kk) {
@@ -194,46 +247,333 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
   }
 
-  // ---- epilogue: normalise, fused combine, LSE ----------------------------
-  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
-  const float inv = 1.0f / ltot;
-  const int64_t tok = (int64_t)b * sq + myq;
-  if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
-  const T* ocrow = outc ? outc + ((int64_t)b * qb + qblk) * D : nullptr;
-  float gtok = 1.f;
-  if (outc && gate_mode == 2) gtok = E::to_f(gate[tok]);
-  // gate row of this token: [BH, Sq, D] (mode 1) or token-major [B, Sq, H, D] (mode 3)
-  const T* grow = nullptr;
-  if (gate_mode == 1) grow = gate + tok * D;
-  if (gate_mode == 3)
-    grow = gate + (((int64_t)(b / gate_heads) * sq + myq) * gate_heads + b % gate_heads) * D;
+  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, lse, outc, gate, gate_mode,
+                     gate_heads);
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong forward for 256-token blocks.  One workgroup of 8 waves owns a whole
+// query block; waves w and w+4 run on the same SIMD.  Group 0 (waves 0-3, rows
+// 0-127) and group 1 (waves 4-7, rows 128-255) do the same per-chunk work half
+// a phase apart, separated by workgroup barriers: while group 0 issues the
+// MFMAs of chunk j (S_j, and O += V_{j-1} P_{j-1}), group 1 runs the softmax of
+// chunk j-1; then group 0 runs the softmax of chunk j while group 1 issues the
+// MFMAs of chunk j.
+// On every SIMD one wave keeps the matrix core busy while the other uses the
+// VALU (an MFMA and VALU work of another wave overlap on CDNA4).  Both groups
+// read the same K/V chunks from a 4-stage LDS ring.
+// Per query row the arithmetic and its order are those of sparse_fwd_kernel:
+// the online-softmax rescale of chunk j follows the PV product of chunk j-1.
+// ---------------------------------------------------------------------------
+template <int D>
+struct FwdPPCfg {
+  static constexpr int NT = 512;
+  static constexpr int KC = 64;
+  static constexpr int TILE = KC * D;
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NS = 4;
+  static constexpr int PER = 2 * (KC * D / 8 / NT);  // direct loads per wave per chunk
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+                     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
+                     T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
+                     const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles,
+                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
+  constexpr int BE = 256;
+  using C = FwdPPCfg<D>;
+  using E = Elem<T>;
+  typedef typename E::vec8 V8;
+  __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
+
+  const int tile = xcd_tile(blockIdx.x, num_tiles);
+  if (tile >= num_tiles) return;
+  const int64_t b = tile / qb;
+  const int qblk = tile % qb;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: group branches are scalar
+  const int r = lane & 31, h = lane >> 5;
+  const bool grp1 = wave >= 4;
+  const int myq = qblk * BE + wave * 32 + r;
+
+  V8 qf[D / 16];
+  {
+    const T* qrow = q + ((int64_t)b * sq + myq) * D + 8 * h;
 #pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = mt * 32 + 8 * g + 4 * h;
-      float val[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) val[e] = oacc[mt][4 * g + e] * inv;
-      if (ocrow) {
-        u32x2 ocr = *reinterpret_cast<const u32x2*>(ocrow + d0);
-        const T* oc = reinterpret_cast<const T*>(&ocr);
-        float gv[4] = {gtok, gtok, gtok, gtok};
-        if (grow) {
-          u32x2 gr = *reinterpret_cast<const u32x2*>(grow + d0);
-          const T* gg = reinterpret_cast<const T*>(&gr);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) gv[e] = E::to_f(gg[e]);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) val[e] = fmaf(E::to_f(oc[e]), gv[e], val[e]);
-      }
-      T o4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = E::from_f(val[e]);
-      *reinterpret_cast<u32x2*>(out + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
+    for (int ks = 0; ks < D / 16; ++ks) {
+      u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + 16 * ks);
+      raw ^= qsign;
+      qf[ks] = as_vec8<T>(raw);
     }
   }
+  const int32_t* sel = selected + ((int64_t)b * qb + qblk) * topk;
+  const T* kbase = k + (int64_t)b * skv * D;
+  const T* vbase = v + (int64_t)b * skv * D;
+  RouteRegs<BE, C::KC> route{sel, kv_vbs, topk, kb};
+  route.load(0);
+  TileDma<T, D, C::KC, C::NT> tdma;
+  tdma.init();
+  int ps = 0, pc = 0, pkv = 0, pnvb = 0;
+  bool pvalid = route.next(ps, pc, pkv, pnvb);
+  // Copy the cursor's chunk into stage stg; returns its valid keys (0: the
+  // route is exhausted and nothing is copied).
+  auto issue = [&](int stg) {
+    int nv = 0;
+    if (pvalid) {
+      const int64_t off = ((int64_t)pkv * BE + pc * C::KC) * D;
+      T* Ks = smem + stg * C::STAGE;
+      tdma.copy(Ks, kbase + off);
+      tdma.copy(Ks + C::TILE, vbase + off);
+      nv = min(pnvb - pc * C::KC, C::KC);
+      ++pc;
+      pvalid = route.next(ps, pc, pkv, pnvb);
+    }
+    return nv;
+  };
+
+  float m = -INFINITY, lsum = 0.f;
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) oacc[mt] = f32x16{};
+  f32x16 sacc[2];
+  V8 pk[4];  // P of the last softmax as B operands, 16 keys each
+
+  // Per-lane LDS byte offsets inside a tile, fixed for the whole kernel.  The
+  // swizzle repeats every 16 rows, so the other rows a lane reads differ from
+  // these by constants (instruction offsets): K rows of key 32*smt + r at
+  // row_off[ks] + 32*smt*D*2, transposed V pieces of keys 16*kk + .. at
+  // tr_off[mt][hi] + 16*kk*D*2.
+  uint32_t row_off[D / 16], tr_off[D / 32][2];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * sizeof(T)));
+  {
+    const int grp = lane >> 4, jl = lane & 15, qq = grp & 1, hh = grp >> 1;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+        tr_off[mt][hi] = opaque((uint32_t)(
+            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3)) *
+            sizeof(T)));
+  }
+  const char* smem_c = reinterpret_cast<const char*>(smem);
+  auto k_row = [&](const char* ks_base, int ks, int smt) {
+    return as_vec8<T>(*reinterpret_cast<const u32x4*>(ks_base + row_off[ks] +
+                                                       smt * 32 * D * (int)sizeof(T)));
+  };
+  auto v_tr = [&](const char* vs_base, int mt, int kk) {
+    const char* base = vs_base + kk * 16 * D * (int)sizeof(T);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][0]));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][1]));
+    u32x4 rr;
+    rr[0] = __builtin_bit_cast(u32x2, lo)[0];
+    rr[1] = __builtin_bit_cast(u32x2, lo)[1];
+    rr[2] = __builtin_bit_cast(u32x2, hi)[0];
+    rr[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return as_vec8<T>(rr);
+  };
+  auto mma_s = [&](int stg) {  // S^T = K Q^T
+    const char* Kb = smem_c + stg * C::STAGE * (int)sizeof(T);
+    sacc[0] = f32x16{};
+    sacc[1] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+      for (int smt = 0; smt < 2; ++smt) sacc[smt] = E::mfma32(k_row(Kb, ks, smt), qf[ks], sacc[smt]);
+  };
+  // The online softmax of a chunk is split between the two phases of its wave.
+  // prep (MFMA phase, under the O products): padding keys to -inf, row max,
+  // the lazy-rescale decision and the exponent arguments t = s*c2 - m, in
+  // place in sacc.  finish (softmax phase): the rescale of O and the row sum,
+  // p = exp2(t), the chunk row sum and the packed P.  The values and their
+  // order are those of sparse_fwd_kernel's softmax.
+  bool resc = false;   // this chunk moved the running max (wave-uniform)
+  float alpha = 1.f;   // exp2(m_old - m_new) when resc
+  float m4[4];
+  float tv[32];        // the chunk's scores, then its exponent arguments
+  auto prep_step = [&](int st, int nv) {  // st in [0, 8): one slice of prep
+    if (st == 0) {
+#pragma unroll
+      for (int x = 0; x < 32; ++x) tv[x] = sacc[x >> 4][x & 15];
+      if (nv < C::KC) {
+        keep_branch();
+#pragma unroll
+        for (int x = 0; x < 32; ++x) {
+          const int key = (x >> 4) * 32 + 8 * ((x & 15) >> 2) + 4 * h + (x & 3);
+          if (key >= nv) tv[x] = -INFINITY;
+        }
+      }
+    }
+    if (st == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m4[i] = tv[i];
+#pragma unroll
+      for (int i = 4; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], tv[i]);
+    }
+    if (st == 2) {
+#pragma unroll
+      for (int i = 16; i < 32; ++i) m4[i & 3] = fmaxf(m4[i & 3], tv[i]);
+    }
+    if (st == 3) {
+      float smax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      smax = pair_max32(smax) * c2;
+      resc = __any(smax > m + kRescaleSlack);
+      const float mnew = resc ? fmaxf(m, smax) : m;
+      alpha = fast_exp2(m - mnew);  // used only when resc
+      m = mnew;
+    }
+    if (st >= 4) {
+      const float negm = -m;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tv[(st - 4) * 8 + i] = fmaf(tv[(st - 4) * 8 + i], c2, negm);
+    }
+  };
+  auto finish = [&](int nv) {
+    if (resc) {
+      lsum *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt) oacc[mt] *= alpha;
+    }
+    float p[2][16];
+#pragma unroll
+    for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) p[smt][i] = fast_exp2(tv[smt * 16 + i]);
+    if (nv < C::KC) {
+      keep_branch();
+#pragma unroll
+      for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (key >= nv) p[smt][i] = 0.f;
+        }
+    }
+    float l4[4] = {0.f, 0.f, 0.f, 0.f};  // chunk row sum in four short chains
+#pragma unroll
+    for (int smt = 0; smt < 2; ++smt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) l4[i & 3] += p[smt][i];
+    lsum += (l4[0] + l4[1]) + (l4[2] + l4[3]);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) pk[kk] = pack8<T>(&p[kk >> 1][8 * (kk & 1)]);
+  };
+  // MFMA phase of chunk j: S_j, then O += V_{j-1} P_{j-1} with prep of chunk j
+  // under it (the S results land while the first O products issue).  Every
+  // LDS operand is read L MFMAs ahead of its use: this wave is the only MFMA
+  // issuer of its SIMD during the phase, so nothing else covers the latency.
+  constexpr int NSX = 2 * (D / 16), NOX = 4 * (D / 32), NX = NSX + NOX, L = 4;
+  auto mma_so = [&](int sj, int sp, int nv) {
+    const char* Kb = smem_c + sj * C::STAGE * (int)sizeof(T);
+    const char* Vb = smem_c + (sp * C::STAGE + C::TILE) * (int)sizeof(T);
+    V8 op[NX];
+    auto load = [&](int u) {  // u < NSX: K row (ks = u >> 1, smt = u & 1); else V^T piece
+      if (u >= NX) return;
+      if (u < NSX) {
+        op[u] = k_row(Kb, u >> 1, u & 1);
+      } else {
+        const int x = u - NSX;  // kk = x / (D/32), mt = x % (D/32)
+        op[u] = v_tr(Vb, x % (D / 32), x / (D / 32));
+      }
+    };
+    sacc[0] = f32x16{};
+    sacc[1] = f32x16{};
+#pragma unroll
+    for (int u = 0; u < L; ++u) load(u);
+#pragma unroll
+    for (int u = 0; u < NX; ++u) {
+      load(u + L);
+      if (u < NSX) {
+        sacc[u & 1] = E::mfma32(op[u], qf[u >> 1], sacc[u & 1]);
+      } else {
+        const int x = u - NSX;
+        oacc[x % (D / 32)] = E::mfma32(op[u], pk[x / (D / 32)], oacc[x % (D / 32)]);
+        // prep slice st after O product x (from the third on: S has landed).
+        // With nv = 0 (the stream's S half on a stale stage) prep masks every
+        // key, so the running max is left as it is.
+        if (x >= 2) {
+          const int st_lo = (x - 2) * 8 / (NOX - 2), st_hi = (x - 1) * 8 / (NOX - 2);
+#pragma unroll
+          for (int st = 0; st < 8; ++st)
+            if (st >= st_lo && st < st_hi) prep_step(st, nv);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto prep_all = [&](int nv) {
+#pragma unroll
+    for (int st = 0; st < 8; ++st) prep_step(st, nv);
+  };
+
+  int nvm1 = 0;        // valid keys of chunk j-1 (0: no such chunk)
+  int nv0 = issue(0);  // chunk j
+  int nv1 = issue(1);  // chunk j+1
+  if (nv1 > 0)
+    wait_vmcnt<C::PER>();
+  else
+    dma_wait();
+  // A phase boundary: the barrier, with the instruction scheduler kept from
+  // moving MFMA or VALU work across it (s_barrier only orders memory, so the
+  // compiler would otherwise let one phase's arithmetic drift into the next).
+  auto phase_barrier = []() {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (grp1) phase_barrier();
+  if (nv0 > 0) {
+    // chunk 0: no chunk -1, so its MFMA phase is S_0 alone
+    phase_barrier();
+    mma_s(0);
+    prep_all(nv0);
+    dma_wait();  // this wave's copies of chunk 1
+    phase_barrier();
+    int nv2 = issue(2);
+    finish(nv0);
+    nvm1 = nv0;
+    nv0 = nv1;
+    nv1 = nv2;
+    // chunks 1 .. n; at j = n (no chunk j) the S half of the stream runs on a
+    // stage no copy is writing and its result is not used
+    for (int j = 1; nvm1 > 0; ++j) {
+      phase_barrier();
+      mma_so(j % C::NS, (j - 1) % C::NS, nv0);
+      dma_wait();  // this wave's copies of chunk j+1
+      phase_barrier();
+      // the stage of chunk j+2 last held chunk j-2, read for the last time in
+      // group 1's MFMA phase of chunk j-1, which ended before this iteration's
+      // first barrier
+      nv2 = issue((j + 2) % C::NS);
+      if (nv0 > 0) finish(nv0);
+      nvm1 = nv0;
+      nv0 = nv1;
+      nv1 = nv2;
+    }
+  }
+  if (!grp1) phase_barrier();
+  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, lse, outc, gate, gate_mode,
+                     gate_heads);
+}
+
+template <typename T, int D>
+static int launch_fwd_pp(const void* q, const void* k, const void* v, const int32_t* selected,
+                         const int32_t* kv_vbs, void* out, float* lse, const void* outc,
+                         const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq,
+                         int64_t skv, int topk, float scale, hipStream_t stream) {
+  const int64_t tiles = bh * (sq / 256);
+  if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
+  const int grid = (int)(((tiles + 7) / 8) * 8);
+  const float c2 = fabsf(scale) * kLog2e;
+  const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
+  hipLaunchKernelGGL((sparse_fwd_pp_kernel<T, D>), dim3(grid), dim3(512), 0, stream,
+                     (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, lse,
+                     (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, (int)sq,
+                     (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign);
+  return vsa_check_launch();
 }
 
 template <typename T, int D, int BE>
@@ -259,6 +599,17 @@ static int launch_fwd(const void* q, const void* k, const void* v, const int32_t
 
 using namespace vsa;
 
+#ifndef VSA_FWD_NO_PP
+// one 8-wave workgroup per query block: used once there are enough blocks to
+// give every CU one (smaller grids run better as 4-wave half-block workgroups)
+#define VSA_FWD_PP_CASE(DD)                                                                    \
+  if (D == DD && be == 256 && bh * (sq / 256) >= 256)                                          \
+    return launch_fwd_pp<T, DD>(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode,   \
+                                gate_heads, bh, sq, skv, topk, scale, s);
+#else
+#define VSA_FWD_PP_CASE(DD)
+#endif
+
 #define VSA_FWD_CASE(DD, BB)                                                                   \
   if (D == DD && be == BB)                                                                     \
     return launch_fwd<T, DD, BB>(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode, gate_heads, \
@@ -279,6 +630,8 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   VSA_DISPATCH_MFMA(dtype, T, {
+    VSA_FWD_PP_CASE(128)
+    VSA_FWD_PP_CASE(64)
     VSA_FWD_CASE(128, 256)
     VSA_FWD_CASE(128, 128)
     VSA_FWD_CASE(128, 64)

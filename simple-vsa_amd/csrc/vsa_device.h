@@ -214,6 +214,11 @@ __device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32
                : "memory");
 }
 
+// An empty side effect that keeps a uniform branch a branch: where the guard is
+// implied by the guarded per-lane conditions (a partial-chunk mask), the
+// compiler would otherwise drop it and run the selects on every iteration.
+__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+
 // Keep a lane-dependent value in a register: the compiler would otherwise
 // rematerialise address arithmetic at every use inside a loop.
 template <typename X>
@@ -262,6 +267,12 @@ struct TileDma {
       voff[i] = opaque((uint32_t)((row * D + c * 8) * sizeof(T)));
     }
   }
+  // piece i of copy(): `src` and `dst` are wave-uniform
+  __device__ __forceinline__ void piece(int i, T* dst, const T* src) const {
+    const uint32_t base =
+        __builtin_amdgcn_readfirstlane(lds_addr(dst) + (uint32_t)(threadIdx.x >> 6) * 1024u);
+    dma16_s(voff[i], src, base + (uint32_t)i * (NT / 64) * 1024u);
+  }
   // `src` and `dst` are wave-uniform
   __device__ __forceinline__ void copy(T* dst, const T* src) const {
     const uint32_t base =
@@ -284,6 +295,20 @@ __device__ __forceinline__ void dma_wait() { wait_vmcnt<0>(); }
 // exp2 on the transcendental unit without the libm range fix-ups
 // (results below 2^-126 flush to zero, which softmax weights tolerate).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Max / sum of the lane pair (i, i ^ 32), in both lanes, with v_permlane32_swap
+// (no LDS round trip, unlike a generic shuffle).  Both are symmetric, so the
+// two swapped halves combine without a select.
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // ---------------------------------------------------------------------------
 // Wave / block reductions (wave64)
@@ -316,6 +341,45 @@ __device__ __forceinline__ float block_reduce(float v, float* red) {
 __device__ __forceinline__ int clamp_valid(int32_t vbs, int be) {
   return vbs < 0 ? 0 : (vbs > be ? be : (int)vbs);
 }
+
+// The route of one query block (its selected key blocks), held in VGPRs 64
+// slots at a time: lane j keeps the key block of slot base + j and its valid
+// token count (0 for an id outside [0, kb)).  Stepping to the next chunk is then
+// a v_readlane with a scalar index instead of two dependent scalar loads from
+// global memory (selected id, then its block size) in front of every copy.
+// load() uses vector loads, so it is only called where no direct-to-LDS copy
+// is in flight (the compiler's vmcnt wait would include them).
+template <int BE, int KC>
+struct RouteRegs {
+  const int32_t* sel;
+  const int32_t* vbs;
+  int topk, kb;
+  int base;  // first slot held (wave-uniform)
+  int rkv, rnv;
+
+  __device__ __forceinline__ void load(int b0) {
+    base = b0;
+    const int j = b0 + (int)(threadIdx.x & 63);
+    const int kv = j < topk ? sel[j] : -1;
+    rkv = kv;
+    rnv = (kv >= 0 && kv < kb) ? clamp_valid(vbs[kv], BE) : 0;
+  }
+  // Advance (s, c) to the next chunk of KC keys that holds a valid key.
+  __device__ __forceinline__ bool next(int& s, int& c, int& kv, int& nvb) {
+    while (s < topk) {
+      if (s - base >= 64) load(s);
+      const int nv = __builtin_amdgcn_readlane(rnv, s - base);
+      if (c * KC < nv) {
+        kv = __builtin_amdgcn_readlane(rkv, s - base);
+        nvb = nv;
+        return true;
+      }
+      ++s;
+      c = 0;
+    }
+    return false;
+  }
+};
 
 // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs
 // of an MI355X, so linear id i runs on XCD i % 8.  Give XCD x the contiguous
