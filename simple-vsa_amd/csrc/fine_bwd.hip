@@ -425,7 +425,21 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
       for (int x = 0; x < L; ++x) issue(x);
       sn = f32x16{};
       pn = f32x16{};
+      // B(i) is spread over the NA MFMAs of A(i+1) and the first NC/2 of C(i):
+      // value x at stream position x * (NA + NC/2) / 16, so that about four
+      // VALU operations sit under each MFMA.  Values 0-7 feed the first half of
+      // C and are done inside A; dS trails P by one value (exp latency).
       float pv[16], dsv[16];
+      auto b_slot = [&](int pos) {
+#pragma unroll
+        for (int x = 0; x < 16; ++x)
+          if (x * (NA + NC / 2) / 16 == pos) {
+            pv[x] = fast_exp2(fmaf(sc[x], c2, -lc[x >> 2][x & 3]));
+            if (x >= 1) dsv[x - 1] = pv[x - 1] * (pc[x - 1] - dc[(x - 1) >> 2][(x - 1) & 3]);
+            if (x == 15) dsv[15] = pv[15] * (pc[15] - dc[3][3]);
+          }
+      };
+      static_assert(8 * (NA + NC / 2) / 16 < NA, "dS 0-7 must be done inside A");
 #pragma unroll
       for (int u = 0; u < NA; ++u) {
         issue(u + L);
@@ -436,19 +450,12 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
           pn = E::mfma32(op[u], vf[u >> 1], pn);
         else
           sn = E::mfma32(op[u], kf[u >> 1], sn);
-#pragma unroll
-        for (int x = (16 * u) / NA; x < (16 * (u + 1)) / NA; ++x) {
-          pv[x] = fast_exp2(fmaf(sc[x], c2, -lc[x >> 2][x & 3]));
-          if (x >= 1) dsv[x - 1] = pv[x - 1] * (pc[x - 1] - dc[(x - 1) >> 2][(x - 1) & 3]);
-        }
+        b_slot(u);
         __builtin_amdgcn_sched_barrier(0);
       }
-      dsv[15] = pv[15] * (pc[15] - dc[3][3]);
       V8 bp[2], bs[2];
       bp[0] = pack8<T>(pv);
-      bp[1] = pack8<T>(pv + 8);
       bs[0] = pack8<T>(dsv);
-      bs[1] = pack8<T>(dsv + 8);
       // descriptor of the copy issued by the next step (its CSR entry is an
       // LDS read; doing it here keeps it off the next step's critical path)
       const int nn = it + NS;
@@ -461,6 +468,11 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
           dkacc[mt] = E::mfma32(op[NA + vv], bs[j], dkacc[mt]);
         else
           dvacc[mt] = E::mfma32(op[NA + vv], bp[j], dvacc[mt]);
+        if (vv < NC / 2) b_slot(NA + vv);
+        if (vv == NC / 2 - 1) {
+          bp[1] = pack8<T>(pv + 8);
+          bs[1] = pack8<T>(dsv + 8);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
