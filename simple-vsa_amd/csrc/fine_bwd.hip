@@ -35,6 +35,56 @@ struct DqCfg {
   static constexpr int STAGE = 2 * TILE;
 };
 
+// dQ epilogue: scale, fold the pooled gradient of the query block
+// (`d_q_c / count`, valid rows only), store.  One lane = one query row,
+// holding dQ^T column r.
+template <typename T, int D, int BE>
+__device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64_t b, int myq,
+                                            int qblk, int h, int sq, int qb, T* __restrict__ dq,
+                                            const T* __restrict__ dqc,
+                                            const int32_t* __restrict__ q_vbs, float scale) {
+  using E = Elem<T>;
+  const int64_t tok = (int64_t)b * sq + myq;
+  const int qpos = myq - qblk * BE;
+  float cdiv = 1.f;
+  bool cvalid = false;
+  const T* crow = nullptr;
+  if (dqc) {
+    const int32_t cnt = q_vbs[qblk];
+    cvalid = qpos < clamp_valid(cnt, BE);
+    cdiv = (float)(cnt > 1 ? cnt : 1);
+    crow = dqc + ((int64_t)b * qb + qblk) * D;
+  }
+  u32x2 cr[D / 32][4];  // loaded together, so their latency is paid once
+  if (cvalid) {
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        cr[mt][g] = *reinterpret_cast<const u32x2*>(crow + mt * 32 + 8 * g + 4 * h);
+  }
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = mt * 32 + 8 * g + 4 * h;
+      float cval[4] = {0.f, 0.f, 0.f, 0.f};
+      if (cvalid) {
+        const T* cc = reinterpret_cast<const T*>(&cr[mt][g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cval[e] = round_t<T>(E::to_f(cc[e]) / cdiv);
+      }
+      T o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float val = round_t<T>(dqacc[mt][4 * g + e] * scale);
+        o4[e] = E::from_f(val + cval[e]);
+      }
+      *reinterpret_cast<u32x2*>(dq + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
+    }
+  }
+}
+
 template <typename T, int D, int BE>
 __global__ __launch_bounds__((DqCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void
 sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -148,38 +198,7 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
   }
 
-  // ---- epilogue: scale, fold the pooled gradient, store ------------------
-  const int qpos = myq - qblk * BE;
-  float cdiv = 1.f;
-  bool cvalid = false;
-  const T* crow = nullptr;
-  if (dqc) {
-    const int32_t cnt = q_vbs[qblk];
-    cvalid = qpos < clamp_valid(cnt, BE);
-    cdiv = (float)(cnt > 1 ? cnt : 1);
-    crow = dqc + ((int64_t)b * qb + qblk) * D;
-  }
-#pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = mt * 32 + 8 * g + 4 * h;
-      float cval[4] = {0.f, 0.f, 0.f, 0.f};
-      if (cvalid) {
-        u32x2 cr = *reinterpret_cast<const u32x2*>(crow + d0);
-        const T* cc = reinterpret_cast<const T*>(&cr);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) cval[e] = round_t<T>(E::to_f(cc[e]) / cdiv);
-      }
-      T o4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float val = round_t<T>(dqacc[mt][4 * g + e] * scale);
-        o4[e] = E::from_f(val + cval[e]);
-      }
-      *reinterpret_cast<u32x2*>(dq + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
-    }
-  }
+  dq_epilogue<T, D, BE>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale);
 }
 
 // ===========================================================================
@@ -534,6 +553,257 @@ epilogue:
   }
 }
 
+// ---------------------------------------------------------------------------
+// Ping-pong dQ for 256-token blocks: the schedule of the 8-wave forward.
+// One workgroup of 8 waves owns a query block; group 0 (waves 0-3) and group 1
+// (waves 4-7) share a SIMD pairwise and run one phase apart:
+//   MFMA phase of chunk j:  dQ^T += K_{j-1}^T dS_{j-1}^T, then
+//                           S_j = K_j Q^T and dP_j = V_j dO^T
+//   VALU phase of chunk j:  P = exp2(S c2 - lse), dS = P (dP - delta), packed.
+// K_j is read as rows in chunk j's phase and transposed in chunk j+1's, V_j
+// only in chunk j's.  Per query row the arithmetic and its order are those of
+// sparse_dq_kernel.
+// ---------------------------------------------------------------------------
+template <int D>
+struct DqPPCfg {
+  static constexpr int NT = 512;
+  static constexpr int KC = 64;
+  static constexpr int TILE = KC * D;
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NS = 4;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+                    const T* __restrict__ dout, const float* __restrict__ lse,
+                    const float* __restrict__ delta, const int32_t* __restrict__ selected,
+                    const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
+                    const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
+                    int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
+                    float scale) {
+  constexpr int BE = 256;
+  using C = DqPPCfg<D>;
+  using E = Elem<T>;
+  typedef typename E::vec8 V8;
+  __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
+
+  const int tile = xcd_tile(blockIdx.x, num_tiles);
+  if (tile >= num_tiles) return;
+  const int64_t b = tile / qb;
+  const int qblk = tile % qb;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const bool grp1 = wave >= 4;
+  const int myq = qblk * BE + wave * 32 + r;
+  const int64_t tok = (int64_t)b * sq + myq;
+
+  V8 qf[D / 16], df[D / 16];
+  {
+    const T* qrow = q + tok * D + 8 * h;
+    const T* drow = dout + tok * D + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + 16 * ks);
+      raw ^= qsign;
+      qf[ks] = as_vec8<T>(raw);
+      df[ks] = as_vec8<T>(*reinterpret_cast<const u32x4*>(drow + 16 * ks));
+    }
+  }
+  const float my_lse = lse[tok];
+  const float my_delta = delta[tok];
+  const int32_t* sel = selected + ((int64_t)b * qb + qblk) * topk;
+  const T* kbase = k + (int64_t)b * skv * D;
+  const T* vbase = v + (int64_t)b * skv * D;
+  RouteRegs<BE, C::KC> route{sel, kv_vbs, topk, kb};
+  route.load(0);
+  TileDma<T, D, C::KC, C::NT> tdma;
+  tdma.init();
+  int ps = 0, pc = 0, pkv = 0, pnvb = 0;
+  bool pvalid = route.next(ps, pc, pkv, pnvb);
+  auto issue = [&](int stg) {  // copy the cursor's chunk; its valid keys (0: none)
+    int nv = 0;
+    if (pvalid) {
+      const int64_t off = ((int64_t)pkv * BE + pc * C::KC) * D;
+      T* Ks = smem + stg * C::STAGE;
+      tdma.copy(Ks, kbase + off);
+      tdma.copy(Ks + C::TILE, vbase + off);
+      nv = min(pnvb - pc * C::KC, C::KC);
+      ++pc;
+      pvalid = route.next(ps, pc, pkv, pnvb);
+    }
+    return nv;
+  };
+
+  // per-lane LDS byte offsets (the swizzle repeats every 16 rows)
+  uint32_t row_off[D / 16], tr_off[D / 32][2];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks)
+    row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * sizeof(T)));
+  {
+    const int grp = lane >> 4, jl = lane & 15, qq = grp & 1, hh = grp >> 1;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+        tr_off[mt][hi] = opaque((uint32_t)(
+            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3)) *
+            sizeof(T)));
+  }
+  const char* smem_c = reinterpret_cast<const char*>(smem);
+  auto t_row = [&](const char* base, int ks, int smt) {  // K or V rows 32*smt + r
+    return as_vec8<T>(*reinterpret_cast<const u32x4*>(base + row_off[ks] +
+                                                       smt * 32 * D * (int)sizeof(T)));
+  };
+  auto t_tr = [&](const char* base, int mt, int kk) {  // K^T pieces, keys 16kk ..
+    const char* bb = base + kk * 16 * D * (int)sizeof(T);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bb + tr_off[mt][0]));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(bb + tr_off[mt][1]));
+    u32x4 rr;
+    rr[0] = __builtin_bit_cast(u32x2, lo)[0];
+    rr[1] = __builtin_bit_cast(u32x2, lo)[1];
+    rr[2] = __builtin_bit_cast(u32x2, hi)[0];
+    rr[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return as_vec8<T>(rr);
+  };
+
+  f32x16 sacc[2], pacc[2], dqacc[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) dqacc[mt] = f32x16{};
+  V8 bs[4];  // dS of the last VALU phase as B operands, 16 keys each
+
+  // MFMA phase: when with_dq, dQ += K_{j-1}^T dS_{j-1}^T first (16 MFMAs, K^T
+  // of stage sp; the packed dS dies before S and dP are written), then S_j and
+  // dP_j (32 MFMAs, K and V rows of stage sj); every LDS operand is read L
+  // MFMAs ahead of its use.
+  constexpr int NSP = 4 * (D / 16), NDQ = 4 * (D / 32), L = 2;
+  auto mma_x = [&](int sj, int sp, auto with_dq) {
+    constexpr int N0 = decltype(with_dq)::value ? NDQ : 0;  // dQ products first
+    constexpr int NX = N0 + NSP;
+    const char* Kb = smem_c + sj * C::STAGE * (int)sizeof(T);
+    const char* Vb = Kb + C::TILE * (int)sizeof(T);
+    const char* Kp = smem_c + sp * C::STAGE * (int)sizeof(T);
+    V8 op[NX];
+    // u < N0: y = u (kk = y / (D/32), mt = y % (D/32)); then x = (u - N0) >> 1
+    // (ks = x >> 1, smt = x & 1), even: K row (S), odd: V row (dP)
+    auto load = [&](int u) {
+      if (u >= NX) return;
+      if (u < N0) {
+        op[u] = t_tr(Kp, u % (D / 32), u / (D / 32));
+      } else {
+        const int x = (u - N0) >> 1;
+        op[u] = t_row(((u - N0) & 1) ? Vb : Kb, x >> 1, x & 1);
+      }
+    };
+#pragma unroll
+    for (int smt = 0; smt < 2; ++smt) sacc[smt] = pacc[smt] = f32x16{};
+#pragma unroll
+    for (int u = 0; u < L; ++u) load(u);
+#pragma unroll
+    for (int u = 0; u < NX; ++u) {
+      load(u + L);
+      if (u < N0) {
+        dqacc[u % (D / 32)] = E::mfma32(op[u], bs[u / (D / 32)], dqacc[u % (D / 32)]);
+      } else {
+        const int x = (u - N0) >> 1;
+        if ((u - N0) & 1)
+          pacc[x & 1] = E::mfma32(op[u], df[x >> 1], pacc[x & 1]);
+        else
+          sacc[x & 1] = E::mfma32(op[u], qf[x >> 1], sacc[x & 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // VALU phase of chunk j: dS^T, packed 16 keys at a time
+  auto valu = [&](int nv) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      float dsv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * (kk & 1) + e;
+        const float p = fast_exp2(fmaf(sacc[kk >> 1][i], c2, -my_lse));
+        dsv[e] = p * (pacc[kk >> 1][i] - my_delta);
+      }
+      if (nv < C::KC) {
+        keep_branch();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = 8 * (kk & 1) + e;
+          const int key = (kk >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (key >= nv) dsv[e] = 0.f;
+        }
+      }
+      bs[kk] = pack8<T>(dsv);
+    }
+  };
+  auto phase_barrier = []() {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using NoDq = std::integral_constant<bool, false>;
+  using WithDq = std::integral_constant<bool, true>;
+
+  // The sequence and the ring protocol of sparse_fwd_pp_kernel: chunk j+1 is
+  // published by the second barrier of group 0's iteration j; the stage of
+  // chunk j+2 last held chunk j-2, whose last reader (group 1's MFMA phase of
+  // chunk j-1, the K^T of the dQ product) finished before the first barrier
+  // of iteration j.
+  int nvm1 = 0;
+  int nv0 = issue(0);
+  int nv1 = issue(1);
+  if (nv1 > 0)
+    wait_vmcnt<2 * TileDma<T, D, C::KC, C::NT>::N>();
+  else
+    dma_wait();
+  if (grp1) phase_barrier();
+  if (nv0 > 0) {
+    phase_barrier();
+    mma_x(0, 0, NoDq{});
+    dma_wait();  // this wave's copies of chunk 1
+    phase_barrier();
+    int nv2 = issue(2);
+    valu(nv0);
+    nvm1 = nv0;
+    nv0 = nv1;
+    nv1 = nv2;
+    // chunks 1 .. n; at j = n (no chunk j) S and dP run on a stage no copy is
+    // writing and their results are not used
+    for (int j = 1; nvm1 > 0; ++j) {
+      phase_barrier();
+      mma_x(j % C::NS, (j - 1) % C::NS, WithDq{});
+      dma_wait();  // this wave's copies of chunk j+1
+      phase_barrier();
+      nv2 = issue((j + 2) % C::NS);
+      if (nv0 > 0) valu(nv0);
+      nvm1 = nv0;
+      nv0 = nv1;
+      nv1 = nv2;
+    }
+  }
+  if (!grp1) phase_barrier();
+  dq_epilogue<T, D, BE>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale);
+}
+
+template <typename T, int D>
+static int launch_dq_pp(const void* q, const void* k, const void* v, const void* dout,
+                        const float* lse, const float* delta, const int32_t* selected,
+                        const int32_t* kv_vbs, void* dq, const void* dqc, const int32_t* q_vbs,
+                        int64_t bh, int64_t sq, int64_t skv, int topk, float scale,
+                        hipStream_t stream) {
+  const int64_t tiles = bh * (sq / 256);
+  if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
+  const int grid = (int)(((tiles + 7) / 8) * 8);
+  hipLaunchKernelGGL((sparse_dq_pp_kernel<T, D>), dim3(grid), dim3(512), 0, stream,
+                     (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, selected,
+                     kv_vbs, (T*)dq, (const T*)dqc, q_vbs, (int)tiles, (int)sq, (int)skv,
+                     (int)(sq / 256), (int)(skv / 256), topk, fabsf(scale) * kLog2e,
+                     scale < 0.f ? 0x80008000u : 0u, scale);
+  return vsa_check_launch();
+}
+
 template <typename T, int D, int BE>
 static int launch_dq(const void* q, const void* k, const void* v, const void* dout,
                      const float* lse, const float* delta, const int32_t* selected,
@@ -590,6 +860,18 @@ extern "C" int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, co
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+#ifndef VSA_DQ_NO_PP
+  // one 8-wave workgroup per query block once every CU gets one
+  if (be == 256 && bh * (sq / 256) >= 256 && (D == 128 || D == 64) &&
+      (dtype == VSA_BF16 || dtype == VSA_F16)) {
+#define VSA_DQ_PP(TT, DD)                                                                    \
+  launch_dq_pp<TT, DD>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, q_vbs, bh, sq, \
+                       skv, topk, scale, s)
+    if (dtype == VSA_BF16) return D == 128 ? VSA_DQ_PP(__bf16, 128) : VSA_DQ_PP(__bf16, 64);
+    return D == 128 ? VSA_DQ_PP(_Float16, 128) : VSA_DQ_PP(_Float16, 64);
+#undef VSA_DQ_PP
+  }
+#endif
 #define VSA_DQ_CASE(DD, BB)                                                                  \
   if (D == DD && be == BB)                                                                   \
     return launch_dq<T, DD, BB>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, q_vbs, \
