@@ -226,6 +226,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
   const int64_t gbase = gate_mode == 3
                             ? ((bh / gate_heads) * sq * gate_heads + bh % gate_heads) * D + c0
                             : 0;
+#pragma unroll 4
   for (int t = row0; t < be; t += rpi) {
     const int64_t tok = blk * be + t;
     const int64_t off = tok * D + c0;
@@ -249,19 +250,20 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       for (int e = 0; e < VEC; ++e) gv[e] = gs;
     }
     float dl = 0.f, dg = 0.f;
+    T dgv[VEC];  // this chunk of d_gate (full gate), stored with one 16-byte write
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float dov = Elem<T>::to_f(g[e]);
       const float attn = outc ? Elem<T>::to_f(o[e]) - oc[e] * gv[e] : Elem<T>::to_f(o[e]);
       dl = fmaf(attn, dov, dl);
+      dgv[e] = Elem<T>::from_f(dov * oc[e]);
       if (outc) {
         dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[e]);
-        if (gate_mode == 1 || gate_mode == 3)
-          d_gate[goff + e] = Elem<T>::from_f(dov * oc[e]);
-        else
-          dg = fmaf(dov, oc[e], dg);
+        if (gate_mode == 2) dg = fmaf(dov, oc[e], dg);
       }
     }
+    if (outc && (gate_mode == 1 || gate_mode == 3))
+      *reinterpret_cast<u32x4*>(d_gate + goff) = *reinterpret_cast<const u32x4*>(dgv);
     // reduce over the tpr lanes of this row (contiguous lanes)
     for (int o2 = tpr >> 1; o2 > 0; o2 >>= 1) {
       dl += __shfl_xor(dl, o2, 64);
