@@ -31,6 +31,7 @@ struct DqCfg {
   // double buffer is 32 KiB and four workgroups share a CU
   static constexpr int KC = (D == 128 && BE == 64) ? 32 : 64;
   static constexpr int NSM = KC / 32;            // 32-key sub-tiles per chunk
+  static constexpr int WPE = D == 256 ? 1 : 2;    // waves per SIMD the registers are sized for
   static constexpr int TILE = KC * D;            // one K (or V) chunk, swizzled row-major
   static constexpr int STAGE = 2 * TILE;
 };
@@ -86,7 +87,7 @@ __device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64
 }
 
 template <typename T, int D, int BE>
-__global__ __launch_bounds__((DqCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void
+__global__ __launch_bounds__((DqCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(DqCfg<D, BE>::WPE))) void
 sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
                  const T* __restrict__ dout, const float* __restrict__ lse,
                  const float* __restrict__ delta, const int32_t* __restrict__ selected,
@@ -226,9 +227,15 @@ struct DkvCfg {
   static constexpr int TP = TILE / 8 / NT;         // direct loads per thread per tile
   static constexpr int PER = 2 * TP + 1;           // direct loads per thread per item
   static constexpr int SEGMAX = 2048;              // CSR entries staged in LDS
+  // dK/dV dims accumulated per workgroup: all of them up to 128; for head_dim
+  // 256 two workgroups share a key tile, each computing S and dP over all 256
+  // dims and accumulating one 128-dim half of dK and dV (the full accumulators
+  // would not fit next to the K and V fragments)
+  static constexpr int DH = D > 128 ? 128 : D;
+  static constexpr int NSPLIT = D / DH;
   static constexpr int NA = 2 * (D / 16);          // MFMAs of A (S and dP interleaved)
-  static constexpr int NC = 4 * (D / 32);          // MFMAs of C (dV and dK interleaved)
-  static constexpr int L = 12;                     // LDS operand lookahead
+  static constexpr int NC = 4 * (DH / 32);         // MFMAs of C (dV and dK interleaved)
+  static constexpr int L = D > 128 ? 6 : 12;       // LDS operand lookahead
 };
 
 template <typename T, int D, int BE>
@@ -248,8 +255,10 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   __shared__ __attribute__((aligned(16))) float sstat[NS][2][C::QS];  // [stage][lse, delta][query]
   __shared__ int32_t sseg[C::SEGMAX];
 
-  const int tile = xcd_tile(blockIdx.x, num_tiles);
-  if (tile >= num_tiles) return;
+  const int tile_s = xcd_tile(blockIdx.x, num_tiles);
+  if (tile_s >= num_tiles) return;
+  const int tile = tile_s / C::NSPLIT;
+  const int d_off = (tile_s % C::NSPLIT) * C::DH;  // first dK/dV dim of this workgroup
   const int64_t b = tile / tiles_per_head;
   const int k0 = (tile % tiles_per_head) * C::KT;  // first key (within head)
   const int kvblk = k0 / BE;
@@ -291,16 +300,16 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   uint32_t row_off[D / 16];  // A rows: lane (r, h), dims 16ks + 8h .. +7
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks) row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * 2));
-  uint32_t tr_off[D / 32][2];  // C operands: rows 8hi + 4h + e, dims 32mt + 16q + 4g
+  uint32_t tr_off[C::DH / 32][2];  // C operands: rows 8hi + 4h + e, dims d_off + 32mt + 16q + 4g
   {
     const int grp = lane >> 4, jl = lane & 15;
     const int qq = grp & 1, hh = grp >> 1;
 #pragma unroll
-    for (int mt = 0; mt < D / 32; ++mt)
+    for (int mt = 0; mt < C::DH / 32; ++mt)
 #pragma unroll
       for (int hi = 0; hi < 2; ++hi)
         tr_off[mt][hi] = opaque((uint32_t)(
-            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3)) * 2));
+            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), d_off + mt * 32 + 16 * qq + 4 * (jl & 3)) * 2));
   }
   const uint32_t st_off = opaque((uint32_t)(4 * h * 4));
   uint32_t cp_goff[TP], cp_loff[TP];  // direct-load pieces: global offset, LDS block
@@ -358,9 +367,9 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     }
   };
 
-  f32x16 dkacc[D / 32], dvacc[D / 32];
+  f32x16 dkacc[C::DH / 32], dvacc[C::DH / 32];
 #pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt) {
+  for (int mt = 0; mt < C::DH / 32; ++mt) {
     dkacc[mt] = f32x16{};
     dvacc[mt] = f32x16{};
   }
@@ -434,7 +443,7 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
           op[x] = row_read(SN, x & 1, x >> 1);
         } else if (x < NA + NC) {
           const int vv = x - NA;
-          const int j = vv / (2 * (D / 32)), mt = (vv >> 1) % (D / 32);
+          const int j = vv / (2 * (C::DH / 32)), mt = (vv >> 1) % (C::DH / 32);
           op[x] = tr_read(S, (vv & 1) ? 0 : 1, mt, j);
         } else if (x < NA + NC + 4) {
           read_stats(SN, ln, dn, x - NA - NC);
@@ -482,7 +491,7 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 #pragma unroll
       for (int vv = 0; vv < NC; ++vv) {
         issue(NA + vv + L);
-        const int j = vv / (2 * (D / 32)), mt = (vv >> 1) % (D / 32);
+        const int j = vv / (2 * (C::DH / 32)), mt = (vv >> 1) % (C::DH / 32);
         if (vv & 1)
           dkacc[mt] = E::mfma32(op[NA + vv], bs[j], dkacc[mt]);
         else
@@ -521,10 +530,10 @@ epilogue:
   const T* kcrow = dkc ? dkc + ((int64_t)b * kb + kvblk) * D : nullptr;
   const T* vcrow = dvc ? dvc + ((int64_t)b * kb + kvblk) * D : nullptr;
 #pragma unroll
-  for (int mt = 0; mt < D / 32; ++mt) {
+  for (int mt = 0; mt < C::DH / 32; ++mt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int d0 = mt * 32 + 8 * g + 4 * h;
+      const int d0 = d_off + mt * 32 + 8 * g + 4 * h;
       float ck[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
       if (key_valid && kcrow) {
         u32x2 a = *reinterpret_cast<const u32x2*>(kcrow + d0);
@@ -831,7 +840,7 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
                        int64_t sq, int64_t skv, int topk, float scale, hipStream_t stream) {
   using C = DkvCfg<D, BE>;
   const int tph = (int)(skv / C::KT);
-  const int64_t tiles = bh * tph;
+  const int64_t tiles = bh * tph * C::NSPLIT;
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   const int grid = (int)(((tiles + 7) / 8) * 8);
   hipLaunchKernelGGL((sparse_dkdv_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
@@ -846,7 +855,8 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
 
 using namespace vsa;
 
-#define VSA_BWD_SHAPES(X) X(128, 256) X(128, 128) X(128, 64) X(64, 256) X(64, 128) X(64, 64)
+#define VSA_BWD_SHAPES(X) \
+  X(128, 256) X(128, 128) X(128, 64) X(64, 256) X(64, 128) X(64, 64) X(256, 256) X(256, 128) X(256, 64)
 
 extern "C" int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
                                  const float* lse, const float* delta, const int32_t* selected,

@@ -35,6 +35,9 @@ struct FwdCfg {
   // double buffer is 32 KiB and four workgroups share a CU
   static constexpr int KC = (D == 128 && BE == 64) ? 32 : 64;
   static constexpr int NSM = KC / 32;              // 32-key sub-tiles per chunk
+  // waves per SIMD the registers are sized for: head_dim 256 (Q fragments and
+  // O accumulators alone take 192 registers) runs one wave per SIMD
+  static constexpr int WPE = D == 256 ? 1 : 2;
   static constexpr int TILE = KC * D;              // elements of one K (or V) chunk
   static constexpr int STAGE = 2 * TILE;           // K and V
 };
@@ -107,7 +110,7 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
 }
 
 template <typename T, int D, int BE>
-__global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(2))) void sparse_fwd_kernel(
+__global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(FwdCfg<D, BE>::WPE))) void sparse_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
@@ -635,6 +638,9 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
     VSA_FWD_CASE(128, 256)
     VSA_FWD_CASE(128, 128)
     VSA_FWD_CASE(128, 64)
+    VSA_FWD_CASE(256, 256)
+    VSA_FWD_CASE(256, 128)
+    VSA_FWD_CASE(256, 64)
     VSA_FWD_CASE(64, 256)
     VSA_FWD_CASE(64, 128)
     VSA_FWD_CASE(64, 64)

@@ -112,6 +112,13 @@ __device__ __forceinline__ int swz<128>(int r, int c) {
   return r * 128 + ((c ^ (((r & 3) << 2) | ((r >> 2) & 3))) << 3);
 }
 
+// D = 256: a row is two 128-element halves (256 bytes each, one pass over the
+// 64 banks), each swizzled as a D = 128 row.
+template <>
+__device__ __forceinline__ int swz<256>(int r, int c) {
+  return r * 256 + ((c >> 4) << 7) + (((c & 15) ^ (((r & 3) << 2) | ((r >> 2) & 3))) << 3);
+}
+
 template <>
 __device__ __forceinline__ int swz<64>(int r, int c) {
   const int R = r >> 1, C = ((r & 1) << 3) | c;
@@ -178,6 +185,13 @@ template <>
 __device__ __forceinline__ int unswz_row_chunk<128>(int P, int& c) {
   const int row = P >> 4;
   c = (P & 15) ^ (((row & 3) << 2) | ((row >> 2) & 3));
+  return row;
+}
+
+template <>
+__device__ __forceinline__ int unswz_row_chunk<256>(int P, int& c) {
+  const int row = P >> 5, q = P & 31;
+  c = (q & 16) | ((q & 15) ^ (((row & 3) << 2) | ((row >> 2) & 3)));
   return row;
 }
 

@@ -18,8 +18,8 @@ The building blocks (pooling, coarse attention + Top-K, CSR inversion, fine
 forward / backward) are exposed as functions so tests can check each kernel.
 
 The MFMA kernels exist for block volumes 64 / 128 / 256 and head dims 64 /
-128.  Other shapes the reference accepts on the GPU (volume in [1, 128],
-head_dim <= 128; triton_impl.py:379-384) run on the same kernels after a
+128 / 256.  Other shapes the reference accepts on the GPU (volume in [1, 128],
+head_dim <= 256; triton_impl.py:379-384) run on the same kernels after a
 differentiable zero-padding of each block to the next kernel volume and of
 the head dim to the next kernel width (gfx950 row kernels); the softmax scale
 stays 1/sqrt(head_dim) of the caller's tensors.  Padded query rows are
@@ -40,7 +40,7 @@ from . import _lib
 from .tiling import _move, _zero_unmarked
 
 SUPPORTED_BLOCKS = (64, 128, 256)
-SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_HEAD_DIMS = (64, 128, 256)
 MFMA_DTYPES = (torch.bfloat16, torch.float16)
 
 
@@ -110,9 +110,9 @@ def _kernel_dim(d: int) -> int:
     """Head dim the kernels run for a caller's head dim ``d``."""
     if d in SUPPORTED_HEAD_DIMS:
         return d
-    if not 1 <= d <= 128:
-        raise ValueError("the MI355X kernels support head_dim <= 128")
-    return 64 if d <= 64 else 128
+    if not 1 <= d <= 256:
+        raise ValueError("the MI355X kernels support head_dim <= 256")
+    return 64 if d <= 64 else 128 if d <= 128 else 256
 
 
 @functools.lru_cache(maxsize=32)

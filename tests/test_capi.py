@@ -112,9 +112,10 @@ def test_kernel_shape_mapping_and_limits():
     assert M._kernel_block(256) == 256 and M._kernel_block(64) == 64
     assert M._kernel_block(27) == 64 and M._kernel_block(100) == 128 and M._kernel_block(1) == 64
     assert M._kernel_dim(80) == 128 and M._kernel_dim(32) == 64 and M._kernel_dim(128) == 128
+    assert M._kernel_dim(129) == 256 and M._kernel_dim(192) == 256 and M._kernel_dim(256) == 256
     with pytest.raises(ValueError, match=r"\[1, 128\] or 256"):
         M._kernel_block(200)
     with pytest.raises(ValueError, match="head_dim"):
-        M._kernel_dim(256)
+        M._kernel_dim(257)
     rows = M._block_rows(12, 3, 64, torch.device("cpu"))
     assert rows.tolist() == [0, 1, 2, 64, 65, 66, 128, 129, 130, 192, 193, 194]

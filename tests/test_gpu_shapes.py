@@ -1,6 +1,7 @@
 """Shapes without a kernel of their own (block volume not in {64, 128, 256},
-head_dim not in {64, 128}) run on the kernels after zero padding; checked
-against the oracle on the caller's shapes."""
+head_dim not in {64, 128, 256}) run on the kernels after zero padding, and the
+head_dim 256 kernels directly; checked against the oracle on the caller's
+shapes."""
 
 import math
 
@@ -15,7 +16,11 @@ DEV = "cuda"
 CASES = [((1, 1, 16), 64, 8, 3, "full"), ((3, 3, 3), 32, 6, 2, "token"),
          ((1, 1, 100), 128, 6, 3, None), ((2, 4, 4), 80, 10, 4, "full"),
          ((4, 4, 4), 48, 8, 3, "token"), ((4, 8, 8), 96, 4, 2, "full"),
-         ((1, 1, 128), 40, 5, 2, None)]
+         ((1, 1, 128), 40, 5, 2, None),
+         # head_dim 256 kernels (dK/dV split over two workgroups per key tile),
+         # natively and for head dims padded up to 256
+         ((4, 8, 8), 256, 4, 2, "full"), ((2, 8, 8), 256, 6, 3, "token"),
+         ((1, 1, 64), 192, 8, 3, None), ((3, 3, 3), 200, 6, 2, "full")]
 
 
 @pytest.fixture(autouse=True)
