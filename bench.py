@@ -46,6 +46,10 @@ WORKLOADS = {
     # 87.5 % sparsity (64-token blocks, topk 80)
     "t444": dict(name="c3 sequence with FastVideo (4,4,4) tiles", B=1, H=40, S=40960, D=128,
                  block=(4, 4, 4), topk=80, gate="full"),
+    # not a BASELINE row: head_dim 256 at the c3 sequence and sparsity, half the heads
+    # (the same FLOPs as c3)
+    "d256": dict(name="c3 sequence at head_dim 256", B=1, H=20, S=40960, D=256,
+                 block=(4, 8, 8), topk=20, gate="full"),
 }
 
 
