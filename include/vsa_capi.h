@@ -118,7 +118,7 @@ int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
  *   out = T(out_c[block] * gate + attn)   (gate = 1 when gate_mode == NONE)
  *   out = T(attn)                          when out_c == NULL
  *   lse[bh, q] = log2(sum_j exp2(scale*log2(e) * q.k_j))   (may be NULL)
- * block_elements in {64, 128, 256}; head_dim in {64, 128}.
+ * block_elements in {64, 128, 256}; head_dim in {64, 128, 256}.
  */
 int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                    const int32_t* selected, const int32_t* kv_vbs,
