@@ -28,6 +28,7 @@ sys.path.insert(0, os.path.join(ROOT, "simple-vsa_amd"))
 
 MFMA_BF16_PEAK_TFLOPS = 2516.6   # MI355X dense bf16
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3      # MI355X published dense fp32
 
 CFG = dict(B=1, H=40, S=40960, D=128, block=(4, 8, 8), topk=20)
 
@@ -50,6 +51,9 @@ WORKLOADS = {
     # (the same FLOPs as c3)
     "d256": dict(name="c3 sequence at head_dim 256", B=1, H=20, S=40960, D=256,
                  block=(4, 8, 8), topk=20, gate="full"),
+    # not a BASELINE row: the c3 shape with fp32 inputs (fp32 vector-ALU kernels)
+    "c3f32": dict(name="Video-DiT mid shape in fp32", B=1, H=40, S=40960, D=128,
+                  block=(4, 8, 8), topk=20, gate="full", dtype="fp32"),
 }
 
 
@@ -119,15 +123,16 @@ def run_workload(key, steps, warmup):
     be = math.prod(w["block"])
     nb = S // be
     amp = w.get("amp", 1.0)
+    dt = {"bf16": torch.bfloat16, "fp32": torch.float32}[w.get("dtype", "bf16")]
     g = torch.Generator(device=dev).manual_seed(0)
-    q, k, v = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16) * amp
+    q, k, v = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=dt) * amp
                for _ in range(3))
-    do = torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    do = torch.randn(B, H, S, D, generator=g, device=dev, dtype=dt)
     gate = None
     if w["gate"] == "full":
-        gate = torch.rand(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+        gate = torch.rand(B, H, S, D, generator=g, device=dev, dtype=dt)
     elif w["gate"] == "token":
-        gate = torch.rand(B, H, S, 1, generator=g, device=dev, dtype=torch.bfloat16)
+        gate = torch.rand(B, H, S, 1, generator=g, device=dev, dtype=dt)
     vbs = torch.full((nb,), be, dtype=torch.int32)
     if "last_valid" in w:
         vbs[-1] = w["last_valid"]
@@ -163,11 +168,15 @@ def run_workload(key, steps, warmup):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     fms = _events_time(fwd_only, max(5, steps // 2))
     F = flops_fwd(B, H, S, D, be, topk)   # padded volume, selected pairs only
-    return {"workload": key, "name": w["name"], "ms_fwd_bwd": round(ms, 3), "ms_fwd": round(fms, 3),
+    return {"workload": key, "name": w["name"], "dtype": w.get("dtype", "bf16"),
+            "ms_fwd_bwd": round(ms, 3), "ms_fwd": round(fms, 3),
             "tflops_fwd_bwd": round(3.5 * F / (ms * 1e-3) / 1e12, 1),
             "tflops_fwd": round(F / (fms * 1e-3) / 1e12, 1),
             "pct_bf16_peak_fwd_bwd": round(100 * 3.5 * F / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 2),
-            "peak_hbm_gib_beyond_inputs": round(peak / 2 ** 30, 3), "steps": steps}
+            "peak_hbm_gib_beyond_inputs": round(peak / 2 ** 30, 3), "steps": steps,
+            **({"pct_fp32_peak_fwd_bwd": round(100 * 3.5 * F / (ms * 1e-3) / 1e12
+                                               / FP32_PEAK_TFLOPS, 2)}
+               if dt == torch.float32 else {})}
 
 
 def run_tiling(steps, warmup):

@@ -13,8 +13,8 @@
  *    no framework types cross this boundary;
  *  - tensors are contiguous row-major; q-like tensors are [BH, Sq, D], k/v-like
  *    [BH, Skv, D], block vectors [BH, nblocks, D], where BH = batch * heads;
- *  - dtype: VSA_BF16 or VSA_F16 for every kernel; VSA_F32 is accepted by the
- *    bandwidth kernels (pooling, coarse, Top-K, CSR, combine/prep) only;
+ *  - dtype: VSA_BF16, VSA_F16 or VSA_F32 for every kernel (the fine kernels
+ *    run bf16 / fp16 on MFMA and fp32 on fp32 kernels, same results contract);
  *  - nothing here allocates or frees device memory: every output and every
  *    workspace buffer is owned by the caller;
  *  - launches are asynchronous on `stream`; no host synchronisation;

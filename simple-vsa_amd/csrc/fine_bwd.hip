@@ -14,6 +14,7 @@
 //   S = Q K^T,  dP = dO V^T,  dS = P (dP - delta),  dV^T += dO^T P,  dK^T += Q^T dS
 #include <type_traits>
 
+#include "fine_f32.h"
 #include "vsa_device.h"
 #include "vsa_launch.h"
 
@@ -870,6 +871,9 @@ extern "C" int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, co
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == VSA_F32)
+    return sparse_dq_f32(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, q_vbs, bh, sq,
+                         skv, D, be, topk, scale, s);
 #ifndef VSA_DQ_NO_PP
   // one 8-wave workgroup per query block once every CU gets one
   if (be == 256 && bh * (sq / 256) >= 256 && (D == 128 || D == 64) &&
@@ -906,6 +910,9 @@ extern "C" int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v,
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == VSA_F32)
+    return sparse_dkdv_f32(q, k, v, dout, lse, delta, counts, offsets, inverse, kv_vbs, dk, dv,
+                           d_k_c, d_v_c, bh, sq, skv, D, be, topk, scale, s);
 #define VSA_DKDV_CASE(DD, BB)                                                                \
   if (D == DD && be == BB)                                                                   \
     return launch_dkdv<T, DD, BB>(q, k, v, dout, lse, delta, counts, offsets, inverse,       \

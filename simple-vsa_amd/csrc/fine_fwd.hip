@@ -21,6 +21,7 @@
 // is only moved when a chunk exceeds it by more than 2^kRescaleSlack (the
 // exponentials stay <= 2^8, exact in fp32 and within bf16 range), so the O
 // rescale runs on a few chunks instead of most.
+#include "fine_f32.h"
 #include "vsa_device.h"
 #include "vsa_launch.h"
 
@@ -632,6 +633,9 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == VSA_F32)
+    return sparse_fwd_f32(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode,
+                          gate_heads, bh, sq, skv, D, be, topk, scale, s);
   VSA_DISPATCH_MFMA(dtype, T, {
     VSA_FWD_PP_CASE(128)
     VSA_FWD_PP_CASE(64)

@@ -17,8 +17,9 @@ stream, with no device synchronisation.
 The building blocks (pooling, coarse attention + Top-K, CSR inversion, fine
 forward / backward) are exposed as functions so tests can check each kernel.
 
-The MFMA kernels exist for block volumes 64 / 128 / 256 and head dims 64 /
-128 / 256.  Other shapes the reference accepts on the GPU (volume in [1, 128],
+The kernels exist for block volumes 64 / 128 / 256 and head dims 64 / 128 /
+256; bf16 / fp16 run on the MFMA kernels, fp32 on fp32 vector-ALU kernels
+(no rounding below fp32 anywhere on its path).  Other shapes the reference accepts on the GPU (volume in [1, 128],
 head_dim <= 256; triton_impl.py:379-384) run on the same kernels after a
 differentiable zero-padding of each block to the next kernel volume and of
 the head dim to the next kernel width (gfx950 row kernels); the softmax scale
@@ -41,7 +42,7 @@ from .tiling import _move, _zero_unmarked
 
 SUPPORTED_BLOCKS = (64, 128, 256)
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
-MFMA_DTYPES = (torch.bfloat16, torch.float16)
+KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
 # ---------------------------------------------------------------------------
@@ -91,8 +92,8 @@ def _check_device_path(q, k, v, block_elements) -> None:
         raise ValueError("q, k, and v must be on the same GPU device")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k, and v must have the same dtype")
-    if q.dtype not in MFMA_DTYPES:
-        raise ValueError("the MI355X kernels support float16 and bfloat16")
+    if q.dtype not in KERNEL_DTYPES:
+        raise ValueError("the MI355X kernels support float16, bfloat16 and float32")
     _kernel_block(block_elements)
     _kernel_dim(q.shape[-1])
 

@@ -57,7 +57,9 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
                               1, 96, 96, 128, 96, 1, 0.1, 0, None) == -4     # be 96: no kernel
     assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
-                              1, 64, 64, 128, 64, 1, 0.1, 2, None) == -3     # fp32 on MFMA path
+                              1, 64, 64, 128, 64, 1, 0.1, 7, None) == -3     # no dtype 7
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
+                              1, 96, 96, 128, 96, 1, 0.1, 2, None) == -4     # fp32, be 96
     # token-major gate: the heads count must divide batch*heads
     assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, p, p, 3, 3,
                               4, 64, 64, 128, 64, 1, 0.1, 0, None) == -2
