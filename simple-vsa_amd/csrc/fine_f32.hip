@@ -1,15 +1,25 @@
 // Sparse fine forward, dQ and dK/dV for fp32 inputs (the reference's GPU path
-// accepts fp32: triton_impl.py:375-376).  gfx950 has no fast fp32 matrix
-// instruction (the fp32 MFMA runs at 1/16 of bf16), so these kernels keep
-// every product in fp32 on the vector ALU and are written for exactness of
-// the fp32 arithmetic rather than speed: outputs, LSE (base 2), the fused
-// combine, the pooled-gradient folds and the padding masks follow the bf16 /
-// fp16 kernels of fine_fwd.hip and fine_bwd.hip with T = fp32 (no rounding).
+// accepts fp32: triton_impl.py:375-376).  Every product and sum stays fp32
+// (no operand rounding): outputs, LSE (base 2), the fused combine, the
+// pooled-gradient folds and the padding masks follow the bf16 / fp16 kernels
+// of fine_fwd.hip and fine_bwd.hip with T = fp32.
 //
-// Layout: a workgroup owns 64 rows (queries, or keys for dK/dV), four lanes
-// per row, each lane holding D/4 consecutive dims; a dot product is a lane
-// partial plus two quad exchanges.  The other operand streams through LDS in
-// chunks of 32 rows, single-buffered.
+// The products run on v_mfma_f32_32x32x2_f32 (the fp32 matrix core: 1/16 of
+// the bf16 rate, twice the unpacked fp32 VALU rate).  Its operands are one
+// float per lane:
+//   A (32 x 2): lane (r, h) = row r, k = h;  B (2 x 32): lane (c, h) = column c, k = h;
+//   C (32 x 32): element i of lane (c, h) = row 8(i/4) + 4h + i%4, column c.
+// A dot product over D dims is D/2 MFMAs; k-step t pairs dim t (h = 0) with
+// dim D/2 + t (h = 1), so each lane reads its row contiguously.  The C tile of
+// one product is the B operand of the next with no data movement (element t of
+// the accumulator is the k = h value of k-step t, rows 8(t/4) + 4h + t%4), and
+// the other operand is read in that row order.
+//
+// Work decomposition as in the bf16 kernels: 32 rows (queries, or keys for
+// dK/dV) per wave, two waves per workgroup; the streamed operand goes through
+// LDS in 32-row chunks (rows padded by 4 floats so that the row reads of 32
+// lanes hit distinct banks).  dK/dV at head_dim 256 (whose fragments and
+// accumulators would exceed a wave's registers) keeps a vector-ALU kernel.
 #include "fine_f32.h"
 #include "vsa_device.h"
 #include "vsa_launch.h"
@@ -21,14 +31,32 @@ namespace {
 constexpr int kRows = 64;   // rows per workgroup
 constexpr int kChunk = 32;  // streamed rows per LDS chunk
 
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ float quad_sum(float x) {
   x += __shfl_xor(x, 1, 64);
   x += __shfl_xor(x, 2, 64);
   return x;
 }
 
-// Copy `rows` rows of D floats (row stride D) into LDS; rows past `valid`
-// are zero (they are never used for a valid result, only kept finite).
+// Copy 32 rows of D floats (global row stride D) into LDS with row stride LD;
+// rows past `valid` are zero (never used for a valid result, only kept finite).
+template <int D, int LD, int NT>
+__device__ __forceinline__ void stage32(float* dst, const float* __restrict__ src, int valid) {
+  constexpr int V4 = D / 4;  // float4 per row
+#pragma unroll 4
+  for (int x = threadIdx.x; x < kChunk * V4; x += NT) {
+    const int r = x / V4, c = x % V4;
+    f32x4 val = {0.f, 0.f, 0.f, 0.f};
+    if (r < valid) val = *reinterpret_cast<const f32x4*>(src + (int64_t)r * D + 4 * c);
+    *reinterpret_cast<f32x4*>(dst + r * LD + 4 * c) = val;
+  }
+}
+
+// Copy `rows` rows of D floats (row stride D) into LDS (row stride D) with 256
+// threads; rows past `valid` are zero.
 template <int D>
 __device__ __forceinline__ void stage_rows_f32(float* dst, const float* __restrict__ src,
                                                int rows, int valid) {
@@ -41,37 +69,87 @@ __device__ __forceinline__ void stage_rows_f32(float* dst, const float* __restri
   }
 }
 
+// this lane's row fragment: x[row][h * D/2 + t], t < D/2
+template <int D>
+__device__ __forceinline__ void load_frag(float (&f)[D / 2], const float* __restrict__ row, int h) {
+#pragma unroll
+  for (int t = 0; t < D / 2; t += 4) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + h * (D / 2) + t);
+    f[t] = x[0]; f[t + 1] = x[1]; f[t + 2] = x[2]; f[t + 3] = x[3];
+  }
+}
+
+// acc += rows(lds, 32 x D, stride LD) . frag^T: A = LDS row r (lane r), B = frag
+template <int D, int LD>
+__device__ __forceinline__ void mma_rows(f32x16& acc, const float* lds, const float (&f)[D / 2],
+                                         int r, int h) {
+  const float* row = lds + r * LD + h * (D / 2);
+#pragma unroll
+  for (int t = 0; t < D / 2; t += 4) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(row + t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = mfma_f32(a[e], f[t + e], acc);
+  }
+}
+
+// acc[mt] += (LDS rows)^T . B, B = the C tile `bop` (rows 8(t/4) + 4h + t%4 of
+// the LDS tile paired with k-step t): A = LDS[row(t, h)][32 mt + r]
+template <int D, int LD>
+__device__ __forceinline__ void mma_cols(f32x16 (&acc)[D / 32], const float* lds, const f32x16& bop,
+                                         int r, int h) {
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const float* row = lds + (8 * (t >> 2) + 4 * h + (t & 3)) * LD + r;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt) acc[mt] = mfma_f32(row[32 * mt], bop[t], acc[mt]);
+  }
+}
+
 }  // namespace
+
+template <int D>
+struct F32Cfg {
+  static constexpr int LD = D + 4;                 // LDS row stride (floats)
+  static constexpr int NT = 128;                   // two waves
+  // waves per SIMD the registers are sized for: forward and dQ hold two D/2
+  // fragments or accumulators of D/32 tiles, dK/dV four
+  static constexpr int WPE_FWD = D <= 128 ? 2 : 1;
+  static constexpr int WPE_DQ = D <= 64 ? 2 : 1;
+  static constexpr int WPE_KV = D <= 64 ? 2 : 1;
+};
 
 // ---------------------------------------------------------------------------
 // Forward: out = softmax(q k^T scale) v over the selected blocks, LSE base 2,
-// combine `out_c * gate` in the epilogue.  grid: bh * Sq / 64.
+// combine `out_c * gate` in the epilogue.  Per wave and 32-key chunk:
+//   S^T = K Q^T (D/2 MFMAs), online softmax per lane-query (lane halves hold
+//   16 keys each, joined by a permlane swap), O^T += V^T P^T (16 D/32 MFMAs).
+// grid: bh * Sq / 64.
 // ---------------------------------------------------------------------------
 template <int D, int BE>
-__global__ __launch_bounds__(256) void sparse_fwd_f32_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
-    float* __restrict__ out, float* __restrict__ lse, const float* __restrict__ outc,
-    const float* __restrict__ gate, int gate_mode, int gate_heads, int tiles_per_head, int sq,
-    int skv, int qb, int kb, int topk, float c2) {
-  constexpr int DS = D / 4;
-  __shared__ __attribute__((aligned(16))) float ks[kChunk * D];
-  __shared__ __attribute__((aligned(16))) float vs[kChunk * D];
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(F32Cfg<D>::WPE_FWD))) void
+sparse_fwd_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                       const float* __restrict__ v, const int32_t* __restrict__ selected,
+                       const int32_t* __restrict__ kv_vbs, float* __restrict__ out,
+                       float* __restrict__ lse, const float* __restrict__ outc,
+                       const float* __restrict__ gate, int gate_mode, int gate_heads,
+                       int tiles_per_head, int sq, int skv, int qb, int kb, int topk, float c2) {
+  using C = F32Cfg<D>;
+  constexpr int LD = C::LD;
+  __shared__ __attribute__((aligned(16))) float ks[kChunk * LD];
+  __shared__ __attribute__((aligned(16))) float vs[kChunk * LD];
   const int64_t b = blockIdx.x / tiles_per_head;
   const int q0 = (blockIdx.x % tiles_per_head) * kRows;
   const int qblk = q0 / BE;
-  const int row = threadIdx.x >> 2, sl = threadIdx.x & 3;
-  const int myq = q0 + row;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int myq = q0 + wave * 32 + r;
   const int64_t tok = b * sq + myq;
-  float qv[DS], o[DS];
+  float qf[D / 2];
+  load_frag<D>(qf, q + tok * D, h);
+  f32x16 o[D / 32];
 #pragma unroll
-  for (int i = 0; i < DS; i += 4) {
-    const f32x4 x = *reinterpret_cast<const f32x4*>(q + tok * D + sl * DS + i);
-    qv[i] = x[0]; qv[i + 1] = x[1]; qv[i + 2] = x[2]; qv[i + 3] = x[3];
-  }
-#pragma unroll
-  for (int i = 0; i < DS; ++i) o[i] = 0.f;
-  float m = -INFINITY, l = 0.f;
+  for (int mt = 0; mt < D / 32; ++mt) o[mt] = f32x16{};
+  float m = -INFINITY, l = 0.f;  // running max (log2 units), this half's partial sum
   const int32_t* sel = selected + (b * qb + qblk) * topk;
   const float* kbase = k + b * (int64_t)skv * D;
   const float* vbase = v + b * (int64_t)skv * D;
@@ -82,83 +160,97 @@ __global__ __launch_bounds__(256) void sparse_fwd_f32_kernel(
     for (int c0 = 0; c0 < nvb; c0 += kChunk) {
       const int nk = min(kChunk, nvb - c0);
       __syncthreads();
-      stage_rows_f32<D>(ks, kbase + ((int64_t)kv * BE + c0) * D, kChunk, nk);
-      stage_rows_f32<D>(vs, vbase + ((int64_t)kv * BE + c0) * D, kChunk, nk);
+      stage32<D, LD, C::NT>(ks, kbase + ((int64_t)kv * BE + c0) * D, nk);
+      stage32<D, LD, C::NT>(vs, vbase + ((int64_t)kv * BE + c0) * D, nk);
       __syncthreads();
-      // all kChunk scores are formed (staged rows past nk are zero) so the
-      // array stays in registers; keys past nk are masked to -inf
-      float sv[kChunk];
+      f32x16 sacc = f32x16{};
+      mma_rows<D, LD>(sacc, ks, qf, r, h);
       float cmax = -INFINITY;
 #pragma unroll
-      for (int kk = 0; kk < kChunk; ++kk) {
-        float d = 0.f;
-#pragma unroll
-        for (int i = 0; i < DS; ++i) d = fmaf(qv[i], ks[kk * D + sl * DS + i], d);
-        sv[kk] = kk < nk ? quad_sum(d) * c2 : -INFINITY;
-        cmax = fmaxf(cmax, sv[kk]);
+      for (int i = 0; i < 16; ++i) {
+        const int key = 8 * (i >> 2) + 4 * h + (i & 3);
+        sacc[i] = key < nk ? sacc[i] * c2 : -INFINITY;
+        cmax = fmaxf(cmax, sacc[i]);
       }
-      const float mnew = fmaxf(m, cmax);
+      const float mnew = fmaxf(m, pair_max32(cmax));
       const float alpha = exp2f(m - mnew);
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < DS; ++i) o[i] *= alpha;
       m = mnew;
+      float psum = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < kChunk; ++kk) {
-        const float p = kk < nk ? exp2f(sv[kk] - m) : 0.f;
-        l += p;
-#pragma unroll
-        for (int i = 0; i < DS; ++i) o[i] = fmaf(p, vs[kk * D + sl * DS + i], o[i]);
+      for (int i = 0; i < 16; ++i) {
+        sacc[i] = exp2f(sacc[i] - m);
+        psum += sacc[i];
       }
+      l = l * alpha + psum;
+#pragma unroll
+      for (int mt = 0; mt < D / 32; ++mt) o[mt] *= alpha;
+      mma_cols<D, LD>(o, vs, sacc, r, h);
     }
   }
   // epilogue: normalise, fused combine, LSE
-  const float inv = 1.0f / l;
-  if (lse != nullptr && sl == 0) lse[tok] = m + log2f(l);
-  const float* ocrow = outc ? outc + (b * qb + qblk) * D + sl * DS : nullptr;
+  const float ltot = pair_sum32(l);
+  const float inv = 1.0f / ltot;
+  if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
+  const float* ocrow = outc ? outc + (b * qb + qblk) * D : nullptr;
   const float* grow = nullptr;
   float gtok = 1.f;
-  if (outc && gate_mode == 1) grow = gate + tok * D + sl * DS;
+  if (outc && gate_mode == 1) grow = gate + tok * D;
   if (outc && gate_mode == 2) gtok = gate[tok];
   if (outc && gate_mode == 3)
-    grow = gate + (((b / gate_heads) * sq + myq) * gate_heads + b % gate_heads) * D + sl * DS;
+    grow = gate + (((b / gate_heads) * sq + myq) * gate_heads + b % gate_heads) * D;
 #pragma unroll
-  for (int i = 0; i < DS; ++i) {
-    float val = o[i] * inv;
-    if (ocrow) val = fmaf(ocrow[i], grow ? grow[i] : gtok, val);
-    out[tok * D + sl * DS + i] = val;
+  for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * mt + 8 * g + 4 * h;
+      f32x4 val;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) val[e] = o[mt][4 * g + e] * inv;
+      if (ocrow) {
+        const f32x4 oc = *reinterpret_cast<const f32x4*>(ocrow + d0);
+        const f32x4 gv = grow ? *reinterpret_cast<const f32x4*>(grow + d0)
+                              : f32x4{gtok, gtok, gtok, gtok};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = fmaf(oc[e], gv[e], val[e]);
+      }
+      *reinterpret_cast<f32x4*>(out + tok * D + d0) = val;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// dQ (query-owned): P = exp2(S c2 - lse), dS = P (dP - delta), dQ = scale dS K,
-// plus the pooled gradient d_q_c / count on the block's valid rows.
+// dQ (query-owned): per wave and 32-key chunk S^T = K Q^T, dP^T = V dO^T,
+// P^T = exp2(S^T c2 - lse), dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T;
+// dQ = scale dQ plus the pooled gradient d_q_c / count on the block's valid
+// rows.  grid: bh * Sq / 64.
 // ---------------------------------------------------------------------------
 template <int D, int BE>
-__global__ __launch_bounds__(256) void sparse_dq_f32_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta, const int32_t* __restrict__ selected,
-    const int32_t* __restrict__ kv_vbs, float* __restrict__ dq, const float* __restrict__ dqc,
-    const int32_t* __restrict__ q_vbs, int tiles_per_head, int sq, int skv, int qb, int kb,
-    int topk, float c2, float scale) {
-  constexpr int DS = D / 4;
-  __shared__ __attribute__((aligned(16))) float ks[kChunk * D];
-  __shared__ __attribute__((aligned(16))) float vs[kChunk * D];
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(F32Cfg<D>::WPE_DQ))) void
+sparse_dq_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                      const float* __restrict__ v, const float* __restrict__ dout,
+                      const float* __restrict__ lse, const float* __restrict__ delta,
+                      const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
+                      float* __restrict__ dq, const float* __restrict__ dqc,
+                      const int32_t* __restrict__ q_vbs, int tiles_per_head, int sq, int skv,
+                      int qb, int kb, int topk, float c2, float scale) {
+  using C = F32Cfg<D>;
+  constexpr int LD = C::LD;
+  __shared__ __attribute__((aligned(16))) float ks[kChunk * LD];
+  __shared__ __attribute__((aligned(16))) float vs[kChunk * LD];
   const int64_t b = blockIdx.x / tiles_per_head;
   const int q0 = (blockIdx.x % tiles_per_head) * kRows;
   const int qblk = q0 / BE;
-  const int row = threadIdx.x >> 2, sl = threadIdx.x & 3;
-  const int myq = q0 + row;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int myq = q0 + wave * 32 + r;
   const int64_t tok = b * sq + myq;
-  float qv[DS], dov[DS], acc[DS];
-#pragma unroll
-  for (int i = 0; i < DS; ++i) {
-    qv[i] = q[tok * D + sl * DS + i];
-    dov[i] = dout[tok * D + sl * DS + i];
-    acc[i] = 0.f;
-  }
+  float qf[D / 2], df[D / 2];
+  load_frag<D>(qf, q + tok * D, h);
+  load_frag<D>(df, dout + tok * D, h);
   const float my_lse = lse[tok], my_delta = delta[tok];
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) acc[mt] = f32x16{};
   const int32_t* sel = selected + (b * qb + qblk) * topk;
   const float* kbase = k + b * (int64_t)skv * D;
   const float* vbase = v + b * (int64_t)skv * D;
@@ -169,21 +261,19 @@ __global__ __launch_bounds__(256) void sparse_dq_f32_kernel(
     for (int c0 = 0; c0 < nvb; c0 += kChunk) {
       const int nk = min(kChunk, nvb - c0);
       __syncthreads();
-      stage_rows_f32<D>(ks, kbase + ((int64_t)kv * BE + c0) * D, kChunk, nk);
-      stage_rows_f32<D>(vs, vbase + ((int64_t)kv * BE + c0) * D, kChunk, nk);
+      stage32<D, LD, C::NT>(ks, kbase + ((int64_t)kv * BE + c0) * D, nk);
+      stage32<D, LD, C::NT>(vs, vbase + ((int64_t)kv * BE + c0) * D, nk);
       __syncthreads();
-      for (int kk = 0; kk < nk; ++kk) {
-        float ds = 0.f, dp = 0.f;
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+      mma_rows<D, LD>(sacc, ks, qf, r, h);
+      mma_rows<D, LD>(pacc, vs, df, r, h);
 #pragma unroll
-        for (int i = 0; i < DS; ++i) {
-          ds = fmaf(qv[i], ks[kk * D + sl * DS + i], ds);
-          dp = fmaf(dov[i], vs[kk * D + sl * DS + i], dp);
-        }
-        const float p = exp2f(fmaf(quad_sum(ds), c2, -my_lse));
-        const float dsv = p * (quad_sum(dp) - my_delta);
-#pragma unroll
-        for (int i = 0; i < DS; ++i) acc[i] = fmaf(dsv, ks[kk * D + sl * DS + i], acc[i]);
+      for (int i = 0; i < 16; ++i) {
+        const int key = 8 * (i >> 2) + 4 * h + (i & 3);
+        const float p = key < nk ? exp2f(fmaf(sacc[i], c2, -my_lse)) : 0.f;
+        sacc[i] = p * (pacc[i] - my_delta);
       }
+      mma_cols<D, LD>(acc, ks, sacc, r, h);
     }
   }
   float cdiv = 1.f;
@@ -194,16 +284,122 @@ __global__ __launch_bounds__(256) void sparse_dq_f32_kernel(
     cdiv = (float)(cnt > 1 ? cnt : 1);
   }
 #pragma unroll
-  for (int i = 0; i < DS; ++i) {
-    const float cv = cvalid ? dqc[(b * qb + qblk) * D + sl * DS + i] / cdiv : 0.f;
-    dq[tok * D + sl * DS + i] = acc[i] * scale + cv;
+  for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * mt + 8 * g + 4 * h;
+      f32x4 cv = {0.f, 0.f, 0.f, 0.f};
+      if (cvalid) cv = *reinterpret_cast<const f32x4*>(dqc + (b * qb + qblk) * D + d0);
+      f32x4 val;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) val[e] = acc[mt][4 * g + e] * scale + cv[e] / cdiv;
+      *reinterpret_cast<f32x4*>(dq + tok * D + d0) = val;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV (key-owned over the CSR in-edges of the key block): for every row of
-// every in-edge query block, dV += P dO, dK += dS Q; dK *= scale; pooled
-// gradients folded on valid keys; padding keys get zero.
+// dK / dV (key-owned over the CSR in-edges of the key block), head_dim 64 /
+// 128: per wave (32 keys) and 32-query item S = Q K^T, dP = dO V^T,
+// P = exp2(S c2 - lse), dS = P (dP - delta), dV^T += dO^T P, dK^T += Q^T dS;
+// dK *= scale; pooled gradients folded on valid keys; padding keys get zero.
+// grid: bh * Skv / 64.
+// ---------------------------------------------------------------------------
+template <int D, int BE>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(F32Cfg<D>::WPE_KV))) void
+sparse_dkdv_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                        const float* __restrict__ v, const float* __restrict__ dout,
+                        const float* __restrict__ lse, const float* __restrict__ delta,
+                        const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+                        const int32_t* __restrict__ inverse, const int32_t* __restrict__ kv_vbs,
+                        float* __restrict__ dk, float* __restrict__ dv,
+                        const float* __restrict__ dkc, const float* __restrict__ dvc,
+                        int tiles_per_head, int sq, int skv, int qb, int kb, int topk, float c2,
+                        float scale) {
+  using C = F32Cfg<D>;
+  constexpr int LD = C::LD;
+  __shared__ __attribute__((aligned(16))) float qs[kChunk * LD];
+  __shared__ __attribute__((aligned(16))) float os[kChunk * LD];
+  __shared__ __attribute__((aligned(16))) float ls[kChunk], es[kChunk];
+  const int64_t b = blockIdx.x / tiles_per_head;
+  const int k0 = (blockIdx.x % tiles_per_head) * kRows;
+  const int kvblk = k0 / BE;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int mykey = k0 + wave * 32 + r;
+  const int64_t ktok = b * skv + mykey;
+  const bool key_valid = mykey - kvblk * BE < clamp_valid(kv_vbs[kvblk], BE);
+  float kf[D / 2], vf[D / 2];
+  load_frag<D>(kf, k + ktok * D, h);
+  load_frag<D>(vf, v + ktok * D, h);
+  f32x16 dka[D / 32], dva[D / 32];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) dka[mt] = dva[mt] = f32x16{};
+  const int64_t meta = b * kb + kvblk;
+  const int nedge = counts[meta];
+  const int32_t* seg = inverse + b * (int64_t)qb * topk + offsets[meta];
+  const float* qbase = q + b * (int64_t)sq * D;
+  const float* dbase = dout + b * (int64_t)sq * D;
+  for (int e = 0; e < nedge; ++e) {
+    const int qblock = seg[e];
+    for (int c0 = 0; c0 < BE; c0 += kChunk) {
+      const int qrow0 = qblock * BE + c0;
+      __syncthreads();
+      stage32<D, LD, C::NT>(qs, qbase + (int64_t)qrow0 * D, kChunk);
+      stage32<D, LD, C::NT>(os, dbase + (int64_t)qrow0 * D, kChunk);
+      if (threadIdx.x < kChunk) {
+        ls[threadIdx.x] = lse[b * sq + qrow0 + threadIdx.x];
+        es[threadIdx.x] = delta[b * sq + qrow0 + threadIdx.x];
+      }
+      __syncthreads();
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+      mma_rows<D, LD>(sacc, qs, kf, r, h);   // S  (queries x keys), lane column = key r
+      mma_rows<D, LD>(pacc, os, vf, r, h);   // dP
+      f32x16 ds;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(ls + 8 * g + 4 * h);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(es + 8 * g + 4 * h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 4 * g + j;
+          sacc[i] = exp2f(fmaf(sacc[i], c2, -l4[j]));
+          ds[i] = sacc[i] * (pacc[i] - d4[j]);
+        }
+      }
+      mma_cols<D, LD>(dva, os, sacc, r, h);  // dV^T += dO^T P
+      mma_cols<D, LD>(dka, qs, ds, r, h);    // dK^T += Q^T dS
+    }
+  }
+  const int32_t cnt = kv_vbs[kvblk];
+  const float cdiv = (float)(cnt > 1 ? cnt : 1);
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * mt + 8 * g + 4 * h;
+      f32x4 ck = {0.f, 0.f, 0.f, 0.f}, cv = {0.f, 0.f, 0.f, 0.f};
+      if (key_valid && dkc) {
+        ck = *reinterpret_cast<const f32x4*>(dkc + meta * D + d0);
+        cv = *reinterpret_cast<const f32x4*>(dvc + meta * D + d0);
+      }
+      f32x4 kk, vv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kk[e] = (key_valid ? dka[mt][4 * g + e] * scale : 0.f) + ck[e] / cdiv;
+        vv[e] = (key_valid ? dva[mt][4 * g + e] : 0.f) + cv[e] / cdiv;
+      }
+      *reinterpret_cast<f32x4*>(dk + ktok * D + d0) = kk;
+      *reinterpret_cast<f32x4*>(dv + ktok * D + d0) = vv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV at head_dim 256 on the vector ALU (key-owned over the CSR in-edges
+// of the key block): four lanes per key, each holding 64 dims; for every row of
+// every in-edge query block dV += P dO, dK += dS Q; dK *= scale; pooled
+// gradients folded on valid keys; padding keys get zero.  grid: bh * Skv / 64.
 // ---------------------------------------------------------------------------
 template <int D, int BE>
 __global__ __launch_bounds__(256) void sparse_dkdv_f32_kernel(
@@ -303,7 +499,7 @@ int sparse_fwd_f32(const void* q, const void* k, const void* v, const int32_t* s
   const float c2 = scale * kLog2e;
 #define VSA_F(DD, BB)                                                                        \
   if (D == DD && be == BB) {                                                                 \
-    hipLaunchKernelGGL((sparse_fwd_f32_kernel<DD, BB>), dim3((unsigned)tiles), dim3(256), 0, \
+    hipLaunchKernelGGL((sparse_fwd_f32m_kernel<DD, BB>), dim3((unsigned)tiles), dim3(128), 0, \
                        s, (const float*)q, (const float*)k, (const float*)v, selected, kv_vbs, \
                        (float*)out, lse, (const float*)out_c, (const float*)gate, gate_mode,  \
                        gate_heads, tph, (int)sq, (int)skv, (int)(sq / BB), (int)(skv / BB),  \
@@ -327,7 +523,7 @@ int sparse_dq_f32(const void* q, const void* k, const void* v, const void* dout,
   const float c2 = scale * kLog2e;
 #define VSA_F(DD, BB)                                                                        \
   if (D == DD && be == BB) {                                                                 \
-    hipLaunchKernelGGL((sparse_dq_f32_kernel<DD, BB>), dim3((unsigned)tiles), dim3(256), 0,  \
+    hipLaunchKernelGGL((sparse_dq_f32m_kernel<DD, BB>), dim3((unsigned)tiles), dim3(128), 0, \
                        s, (const float*)q, (const float*)k, (const float*)v,                 \
                        (const float*)dout, lse, delta, selected, kv_vbs, (float*)dq,         \
                        (const float*)dqc, q_vbs, tph, (int)sq, (int)skv, (int)(sq / BB),     \
@@ -349,7 +545,18 @@ int sparse_dkdv_f32(const void* q, const void* k, const void* v, const void* dou
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   const int tph = (int)(skv / kRows);
   const float c2 = scale * kLog2e;
+  // head_dim 64 / 128 on the matrix core, 256 on the vector ALU
 #define VSA_F(DD, BB)                                                                        \
+  if constexpr (DD <= 128) {                                                                 \
+  if (D == DD && be == BB) {                                                                 \
+    hipLaunchKernelGGL((sparse_dkdv_f32m_kernel<DD, BB>), dim3((unsigned)tiles), dim3(128), 0, \
+                       s, (const float*)q, (const float*)k, (const float*)v,                 \
+                       (const float*)dout, lse, delta, counts, offsets, inverse, kv_vbs,     \
+                       (float*)dk, (float*)dv, (const float*)dkc, (const float*)dvc, tph,    \
+                       (int)sq, (int)skv, (int)(sq / BB), (int)(skv / BB), topk, c2, scale); \
+    return vsa_check_launch();                                                               \
+  }                                                                                          \
+  } else {                                                                                   \
   if (D == DD && be == BB) {                                                                 \
     hipLaunchKernelGGL((sparse_dkdv_f32_kernel<DD, BB>), dim3((unsigned)tiles), dim3(256), 0, \
                        s, (const float*)q, (const float*)k, (const float*)v,                 \
@@ -357,6 +564,7 @@ int sparse_dkdv_f32(const void* q, const void* k, const void* v, const void* dou
                        (float*)dk, (float*)dv, (const float*)dkc, (const float*)dvc, tph,    \
                        (int)sq, (int)skv, (int)(sq / BB), (int)(skv / BB), topk, c2, scale); \
     return vsa_check_launch();                                                               \
+  }                                                                                          \
   }
   VSA_F32_SHAPES(VSA_F)
 #undef VSA_F

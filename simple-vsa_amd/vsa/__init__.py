@@ -11,8 +11,8 @@ from typing import Any
 from .gate import CompressionGate
 from .tiling import build_vsa_metadata, tile, untile
 
-__all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_route", "CompressionGate",
-           "build_vsa_metadata", "tile", "untile"]
+__all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_sparse_executor", "mi355x_route",
+           "CompressionGate", "build_vsa_metadata", "tile", "untile"]
 
 
 def mi355x_vsa(*args: Any, **kwargs: Any) -> Any:
@@ -25,6 +25,13 @@ def mi355x_vsa(*args: Any, **kwargs: Any) -> Any:
 def mi355x_sparse_attention(*args: Any, **kwargs: Any) -> Any:
     """Route-explicit sparse executor on MI355X; see ``vsa.mi355x``."""
     from .mi355x import mi355x_sparse_attention as _impl
+
+    return _impl(*args, **kwargs)
+
+
+def mi355x_sparse_executor(*args: Any, **kwargs: Any) -> Any:
+    """Sparse-executor callable for a shared orchestrator; see ``vsa.mi355x``."""
+    from .mi355x import mi355x_sparse_executor as _impl
 
     return _impl(*args, **kwargs)
 

@@ -400,6 +400,21 @@ def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
         return sparse_forward(q, k, v, selected, vbs, be, scale, want_lse=False)[0]
 
 
+def mi355x_sparse_executor(block_size):
+    """The reference's sparse-executor protocol (triton_impl.py:1711-1718,
+    1748-1753): returns ``execute(q, k, v, selected, variable_block_sizes, *,
+    sm_scale)``, the callable an orchestrator such as ``_vsa_with_sparse_executor``
+    (triton_impl.py:1655-1731) invokes for the fine branch, bound to one block
+    volume like the reference's ``execute`` closure."""
+    be = as_block_elements(block_size)
+
+    def execute(q, k, v, selected, variable_block_sizes, *, sm_scale=None):
+        return mi355x_sparse_attention(q, k, v, selected, variable_block_sizes,
+                                       block_size=(1, 1, be), sm_scale=sm_scale)
+
+    return execute
+
+
 # ---------------------------------------------------------------------------
 # Full VSA (torch_vsa / triton_vsa signature)
 # ---------------------------------------------------------------------------

@@ -98,6 +98,11 @@ def test_cpu_tensors_are_rejected_not_computed_elsewhere():
     sel = torch.zeros(1, 1, 2, 1, dtype=torch.int32)
     with pytest.raises(ValueError, match="GPU"):
         M.mi355x_sparse_attention(q, q, q, sel, _full(2, 64), block_size=(1, 1, 64))
+    # the executor protocol (sparse_executor(q, k, v, selected, vbs, *, sm_scale)) goes
+    # through the same checks
+    execute = M.mi355x_sparse_executor((1, 1, 64))
+    with pytest.raises(ValueError, match="GPU"):
+        execute(q, q, q, sel, _full(2, 64), sm_scale=0.125)
 
 
 def test_block_volume_and_gate_shape_helpers():

@@ -268,6 +268,35 @@ def test_negative_and_custom_scale():
         assert_parity(out, ref, what=f"scale {scale}")
 
 
+def test_sparse_executor_protocol():
+    """An orchestrator in the shape of _vsa_with_sparse_executor
+    (triton_impl.py:1655-1731) driving the executor callable: coarse route,
+    then execute(q, k, v, selected, vbs, sm_scale=scale) for the fine branch;
+    the fine branch equals mi355x_sparse_attention on the same route, bitwise,
+    in value and gradient, and matches the oracle."""
+    from vsa import mi355x as M
+    g = torch.Generator().manual_seed(44)
+    be, d, h, nb, tk = 256, 128, 2, 5, 2
+    vbs = torch.tensor([256, 256, 200, 256, 256])
+    q, k, v, do = (_randn((1, h, nb * be, d), g, torch.bfloat16) for _ in range(4))
+    qg, kg, vg, vbs_g, dog = _gpu(q, k, v, vbs, do)
+    _, sel = M.mi355x_route(qg, kg, vg, vbs_g, vbs_g, tk, (4, 8, 8))
+    execute = M.mi355x_sparse_executor((4, 8, 8))
+    scale = 1.0 / math.sqrt(d)
+    outs = []
+    for run in (lambda a, b, c: execute(a, b, c, sel, vbs_g, sm_scale=scale),
+                lambda a, b, c: M.mi355x_sparse_attention(a, b, c, sel, vbs_g,
+                                                          block_size=(4, 8, 8), sm_scale=scale)):
+        leaves = [t.clone().requires_grad_() for t in (qg, kg, vg)]
+        out = run(*leaves)
+        outs.append((out.detach(), torch.autograd.grad(out, leaves, dog)))
+    assert torch.equal(outs[0][0], outs[1][0])
+    for a, b in zip(outs[0][1], outs[1][1]):
+        assert torch.equal(a, b)
+    ref = O.sparse_attention(q, k, v, sel.cpu(), vbs, block_size=(4, 8, 8), sm_scale=scale)
+    assert_parity(outs[0][0], ref, what="executor out")
+
+
 # ---------------------------------------------------------------------------
 # Full VSA vs torch_vsa (tests/test_triton_vsa.py:199-398)
 # ---------------------------------------------------------------------------
