@@ -334,6 +334,7 @@ def main():
         delta, d_outc, _ = M.backward_prep(out, do, be, out_c=outc, gate=gd)
         dqc, dkc, dvc = M.coarse_backward(qc, kc, vc, probs, d_outc, scale)
         inverse, offsets, counts = M.invert_routes(sel, nb)
+        order = M.dkdv_tile_order(counts, B * H, S, D, be)
         from vsa import _lib
         code, st = _lib.dtype_code(qd.dtype), _lib.stream_of(qd)
         dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
@@ -348,7 +349,7 @@ def main():
                       _lib.ptr(do), _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(counts),
                       _lib.ptr(offsets), _lib.ptr(inverse), _lib.ptr(vbs), _lib.ptr(dk),
                       _lib.ptr(dv), _lib.ptr(dkc), _lib.ptr(dvc), B * H, S, S, D, be, topk,
-                      scale, code, st)
+                      scale, _lib.ptr(order), code, st)
 
         it = 10
         kt = {

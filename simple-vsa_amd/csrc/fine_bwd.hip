@@ -247,7 +247,8 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     const int32_t* __restrict__ inverse, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ dk, T* __restrict__ dv, const T* __restrict__ dkc,
     const T* __restrict__ dvc, int num_tiles, int tiles_per_head, int sq, int skv, int qb,
-    int kb, int topk, float c2, uint32_t ksign, float scale) {
+    int kb, int topk, float c2, uint32_t ksign, float scale,
+    const int32_t* __restrict__ tile_order) {
   using C = DkvCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
@@ -256,7 +257,9 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   __shared__ __attribute__((aligned(16))) float sstat[NS][2][C::QS];  // [stage][lse, delta][query]
   __shared__ int32_t sseg[C::SEGMAX];
 
-  const int tile_s = xcd_tile(blockIdx.x, num_tiles);
+  // workgroup i runs on XCD i % 8; tile_order (from dkdv_order_kernel) permutes
+  // each XCD's contiguous tile range, else the range is walked in order
+  const int tile_s = tile_order ? tile_order[blockIdx.x] : xcd_tile(blockIdx.x, num_tiles);
   if (tile_s >= num_tiles) return;
   const int tile = tile_s / C::NSPLIT;
   const int d_off = (tile_s % C::NSPLIT) * C::DH;  // first dK/dV dim of this workgroup
@@ -838,7 +841,8 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
                        const float* lse, const float* delta, const int32_t* counts,
                        const int32_t* offsets, const int32_t* inverse, const int32_t* kv_vbs,
                        void* dk, void* dv, const void* dkc, const void* dvc, int64_t bh,
-                       int64_t sq, int64_t skv, int topk, float scale, hipStream_t stream) {
+                       int64_t sq, int64_t skv, int topk, float scale, const int32_t* tile_order,
+                       hipStream_t stream) {
   using C = DkvCfg<D, BE>;
   const int tph = (int)(skv / C::KT);
   const int64_t tiles = bh * tph * C::NSPLIT;
@@ -848,8 +852,104 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, counts,
                      offsets, inverse, kv_vbs, (T*)dk, (T*)dv, (const T*)dkc, (const T*)dvc,
                      (int)tiles, tph, (int)sq, (int)skv, (int)(sq / BE), (int)(skv / BE), topk,
-                     fabsf(scale) * kLog2e, scale < 0.f ? 0x80008000u : 0u, scale);
+                     fabsf(scale) * kLog2e, scale < 0.f ? 0x80008000u : 0u, scale, tile_order);
   return vsa_check_launch();
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV tile order.  A dK/dV workgroup's work is proportional to the CSR
+// in-edge count of its key block; on skewed routes (hot key blocks chosen by
+// most query blocks) a few workgroups carry many times the average and, if
+// they start late, set the kernel's end.  One workgroup per XCD range (the
+// tiles xcd_tile gives XCD x) checks whether its largest tile exceeds a
+// quarter of what each concurrent workgroup slot of the XCD gets on average;
+// if so it lists the range longest-first (counting sort on the edge count),
+// else in order.  Workgroup i of the dK/dV grid then takes tile_order[i].
+// Only the dispatch order changes: every tile computes the same values, so
+// the order inside a count bin (set by LDS atomics) does not reach the
+// results.
+// ---------------------------------------------------------------------------
+constexpr int kOrderBins = 1024;  // edge counts >= 1023 share the top bin
+
+__global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ order,
+                                                          int num_tiles, int per, int tph,
+                                                          int tpb, int nsplit, int kb,
+                                                          int slots) {
+  __shared__ int bin[kOrderBins];
+  __shared__ long long rsum[16];
+  __shared__ int rmax[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int x = blockIdx.x;
+  const int lo = x * per, n = max(0, min(per, num_tiles - lo));
+  auto nedge_of = [&](int j) {
+    const int tile = (lo + j) / nsplit;
+    return counts[(int64_t)(tile / tph) * kb + (tile % tph) / tpb];
+  };
+  long long sum = 0;
+  int mx = 0;
+  for (int j = tid; j < n; j += 1024) {
+    const int e = nedge_of(j);
+    sum += e;
+    mx = max(mx, e);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    sum += __shfl_xor(sum, o, 64);
+    mx = max(mx, __shfl_xor(mx, o, 64));
+  }
+  if (lane == 0) {
+    rsum[wave] = sum;
+    rmax[wave] = mx;
+  }
+  bin[tid] = 0;
+  __syncthreads();
+  sum = 0;
+  mx = 0;
+  for (int w = 0; w < 16; ++w) {
+    sum += rsum[w];
+    mx = max(mx, rmax[w]);
+  }
+  if ((long long)mx * slots * 4 <= sum) {
+    for (int j = tid; j < per; j += 1024) order[x + 8 * j] = j < n ? lo + j : num_tiles;
+    return;
+  }
+  for (int j = tid; j < n; j += 1024) atomicAdd(&bin[min(nedge_of(j), kOrderBins - 1)], 1);
+  __syncthreads();
+  // start of each bin in descending order: sum of the counts of all larger bins
+  const int c = bin[kOrderBins - 1 - tid];  // thread t holds bin K-1-t
+  int incl = c;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  __shared__ int wtot[16];
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wtot[w];
+  bin[kOrderBins - 1 - tid] = base + incl - c;
+  __syncthreads();
+  for (int j = tid; j < n; j += 1024) {
+    const int pos = atomicAdd(&bin[min(nedge_of(j), kOrderBins - 1)], 1);
+    order[x + 8 * pos] = lo + j;
+  }
+  for (int j = n + tid; j < per; j += 1024) order[x + 8 * j] = num_tiles;
+}
+
+// dK/dV grid geometry of the MFMA kernels for (head_dim, block volume): tiles
+// per (b, h) and per key block, the head-dim split and the workgroups one CU
+// runs at a time
+struct DkvGeometry {
+  int tph, tpb, nsplit, wg_per_cu;
+};
+static bool dkdv_geometry(int D, int be, int64_t skv, DkvGeometry& g) {
+  if (!((D == 64 || D == 128 || D == 256) && (be == 64 || be == 128 || be == 256))) return false;
+  const int kt = be >= 128 ? 128 : be;  // DkvCfg<D, BE>::KT
+  g.tph = (int)(skv / kt);
+  g.tpb = be / kt;
+  g.nsplit = D > 128 ? 2 : 1;
+  g.wg_per_cu = 4 / (kt / 32);          // one wave per SIMD
+  return true;
 }
 
 }  // namespace vsa
@@ -895,13 +995,30 @@ extern "C" int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, co
   return VSA_ERR_UNSUPPORTED;
 }
 
+extern "C" int vsa_dkdv_tile_order(const int32_t* counts, int32_t* tile_order,
+                                   int64_t order_len, int64_t bh, int64_t skv, int32_t D,
+                                   int32_t be, void* stream) {
+  if (!counts || !tile_order) return VSA_ERR_NULL;
+  DkvGeometry g;
+  if (bh <= 0 || skv <= 0 || be <= 0 || skv % be) return VSA_ERR_SHAPE;
+  if (!dkdv_geometry(D, be, skv, g)) return VSA_ERR_UNSUPPORTED;
+  const int64_t tiles = bh * g.tph * g.nsplit;
+  const int64_t per = (tiles + 7) / 8;
+  if (tiles > (1LL << 30) || order_len < 8 * per) return VSA_ERR_SHAPE;
+  hipLaunchKernelGGL(dkdv_order_kernel, dim3(8), dim3(1024), 0, (hipStream_t)stream, counts,
+                     tile_order, (int)tiles, (int)per, g.tph, g.tpb, g.nsplit,
+                     (int)(skv / be), 32 * g.wg_per_cu);
+  return vsa_check_launch();
+}
+
 extern "C" int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v,
                                    const void* dout, const float* lse, const float* delta,
                                    const int32_t* counts, const int32_t* offsets,
                                    const int32_t* inverse, const int32_t* kv_vbs, void* dk,
                                    void* dv, const void* d_k_c, const void* d_v_c, int64_t bh,
                                    int64_t sq, int64_t skv, int32_t D, int32_t be, int32_t topk,
-                                   float scale, int32_t dtype, void* stream) {
+                                   float scale, const int32_t* tile_order, int32_t dtype,
+                                   void* stream) {
   if (!q || !k || !v || !dout || !lse || !delta || !counts || !offsets || !inverse || !kv_vbs ||
       !dk || !dv)
     return VSA_ERR_NULL;
@@ -916,7 +1033,8 @@ extern "C" int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v,
 #define VSA_DKDV_CASE(DD, BB)                                                                \
   if (D == DD && be == BB)                                                                   \
     return launch_dkdv<T, DD, BB>(q, k, v, dout, lse, delta, counts, offsets, inverse,       \
-                                  kv_vbs, dk, dv, d_k_c, d_v_c, bh, sq, skv, topk, scale, s);
+                                  kv_vbs, dk, dv, d_k_c, d_v_c, bh, sq, skv, topk, scale, \
+                                  tile_order, s);
   VSA_DISPATCH_MFMA(dtype, T, { VSA_BWD_SHAPES(VSA_DKDV_CASE) });
 #undef VSA_DKDV_CASE
   return VSA_ERR_UNSUPPORTED;

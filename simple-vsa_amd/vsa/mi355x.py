@@ -43,6 +43,7 @@ from .tiling import _move, _zero_unmarked
 SUPPORTED_BLOCKS = (64, 128, 256)
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
 KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+MFMA_DTYPES = (torch.bfloat16, torch.float16)
 
 
 # ---------------------------------------------------------------------------
@@ -328,12 +329,26 @@ def sparse_backward(q, k, v, dout, lse, delta, selected, variable_block_sizes, b
               _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(selected), _lib.ptr(variable_block_sizes),
               _lib.ptr(dq), _lib.ptr(dqc), _lib.ptr(q_variable_block_sizes), b * h, sq, skv, d,
               block_elements, tk, float(scale), code, stream)
+    order = dkdv_tile_order(counts, b * h, skv, d, block_elements) if q.dtype in MFMA_DTYPES \
+        else None
     _lib.call("vsa_sparse_bwd_dkdv", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(dout),
               _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(counts), _lib.ptr(offsets),
               _lib.ptr(inverse), _lib.ptr(variable_block_sizes), _lib.ptr(dk), _lib.ptr(dv),
               _lib.ptr(dkc), _lib.ptr(dvc), b * h, sq, skv, d, block_elements, tk, float(scale),
-              code, stream)
+              _lib.ptr(order), code, stream)
     return dq, dk, dv
+
+
+def dkdv_tile_order(counts, bh, skv, head_dim, block_elements):
+    """Dispatch order of the bf16/fp16 dK/dV workgroups: each XCD's tile range
+    longest-first when one key block's in-edge count would otherwise set the
+    kernel's end (skewed routes), else in order (see vsa_dkdv_tile_order)."""
+    kt = 128 if block_elements >= 128 else block_elements
+    tiles = bh * (skv // kt) * (2 if head_dim > 128 else 1)
+    order = torch.empty(8 * ((tiles + 7) // 8), device=counts.device, dtype=torch.int32)
+    _lib.call("vsa_dkdv_tile_order", _lib.ptr(counts), _lib.ptr(order), order.numel(), bh, skv,
+              head_dim, block_elements, _lib.stream_of(counts))
+    return order
 
 
 # ---------------------------------------------------------------------------

@@ -64,3 +64,67 @@ def test_long_route_equals_short_route(be, H, D, nb, n_real):
     diff = (a - e).abs().max().item()
     rel = ((a - e).norm() / e.norm()).item()
     assert diff <= 2e-2 and rel <= 1e-2, (diff, rel)
+
+
+def _order_case(H, nb, be, D, hot):
+    """Inputs for the dK/dV dispatch-order checks: `hot` key blocks chosen by
+    every query block (a skewed route), the other slots spread uniformly."""
+    from vsa import mi355x as M
+    g = torch.Generator().manual_seed(nb * 7 + hot)
+    S, tk = nb * be, 4
+    q, k, v, do = (torch.randn(1, H, S, D, generator=g).to(torch.bfloat16).to(DEV)
+                   for _ in range(4))
+    rest = torch.stack([hot + torch.randperm(nb - hot, generator=g)[:tk - hot]
+                        for _ in range(H * nb)]).view(1, H, nb, tk - hot)
+    sel = torch.cat([torch.arange(hot).expand(1, H, nb, hot), rest], -1).to(torch.int32).to(DEV)
+    vbs = torch.full((nb,), be, dtype=torch.int32, device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    out, lse = M.sparse_forward(q, k, v, sel, vbs, be, scale)
+    delta, _, _ = M.backward_prep(out, do, be)
+    inv, off, cnt = M.invert_routes(sel, nb)
+    return M, q, k, v, do, lse, delta, sel, vbs, inv, off, cnt, scale, tk
+
+
+@pytest.mark.parametrize("H,nb,be,D,hot", [(4, 160, 64, 64, 2), (2, 60, 256, 128, 1),
+                                           (3, 40, 128, 256, 2), (16, 160, 256, 128, 0)])
+def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
+    from vsa import _lib
+    M, q, k, v, do, lse, delta, sel, vbs, inv, off, cnt, scale, tk = _order_case(H, nb, be, D, hot)
+    S = nb * be
+    order = M.dkdv_tile_order(cnt, H, S, D, be)
+    kt = 128 if be >= 128 else be
+    nsplit = 2 if D > 128 else 1
+    tiles = H * (S // kt) * nsplit
+    o = order.cpu().numpy()
+    real = o[o < tiles]
+    assert sorted(real.tolist()) == list(range(tiles))        # every tile exactly once
+    assert (o[o >= tiles] == tiles).all()                     # the rest are the sentinel
+    per = (tiles + 7) // 8
+    nedge = cnt.cpu().reshape(H, nb).repeat_interleave(be // kt, 1).reshape(-1)
+    nedge = nedge.repeat_interleave(nsplit)
+    slots = 32 * (4 // (kt // 32))                            # concurrent workgroups per XCD
+    sorted_ranges = 0
+    for x in range(8):                                        # each XCD keeps its own range
+        ids = o[x::8]
+        ids = ids[ids < tiles]
+        assert ((ids >= x * per) & (ids < (x + 1) * per)).all()
+        rng = nedge[x * per:min((x + 1) * per, tiles)]
+        if len(rng) and int(rng.max()) * slots * 4 > int(rng.sum()):   # skewed: longest first
+            e = nedge[torch.from_numpy(ids.astype('int64'))]
+            assert (e[:-1] >= e[1:]).all()
+            sorted_ranges += 1
+        else:                                                 # balanced: index order
+            assert (ids == sorted(ids)).all()
+    assert sorted_ranges > 0 if hot else True
+    # the dispatch order does not reach the results
+    P = lambda t: _lib.ptr(t)
+    res = []
+    for tord in (None, order):
+        dk, dv = torch.empty_like(k), torch.empty_like(v)
+        _lib.call("vsa_sparse_bwd_dkdv", P(q), P(k), P(v), P(do), P(lse), P(delta), P(cnt),
+                  P(off), P(inv), P(vbs), P(dk), P(dv), None, None, H, S, S, D, be, tk,
+                  float(scale), P(tord), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+        res.append((dk, dv))
+    torch.cuda.synchronize()
+    for a, b_ in zip(*res):
+        assert torch.equal(a, b_)
