@@ -55,6 +55,33 @@ __device__ __forceinline__ void stage32(float* dst, const float* __restrict__ sr
   }
 }
 
+// stage32 split in two: load() issues this thread's loads of a 32-row tile
+// into registers, store() writes them to LDS, so the next chunk's loads are in
+// flight while the current one is multiplied (for kernels at one wave per
+// SIMD, where no other wave of the SIMD hides the copy).
+template <int D, int LD, int NT>
+struct Stage32 {
+  static constexpr int V4 = D / 4;
+  static constexpr int N = kChunk * V4 / NT;  // float4 per thread
+  static_assert(kChunk * V4 % NT == 0, "tile must split evenly over the workgroup");
+  f32x4 buf[N];
+  __device__ __forceinline__ void load(const float* __restrict__ src, int valid) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int x = (int)threadIdx.x + i * NT, r = x / V4, c = x % V4;
+      buf[i] = r < valid ? *reinterpret_cast<const f32x4*>(src + (int64_t)r * D + 4 * c)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __device__ __forceinline__ void store(float* dst) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int x = (int)threadIdx.x + i * NT, r = x / V4, c = x % V4;
+      *reinterpret_cast<f32x4*>(dst + r * LD + 4 * c) = buf[i];
+    }
+  }
+};
+
 // Copy `rows` rows of D floats (row stride D) into LDS (row stride D) with 256
 // threads; rows past `valid` are zero.
 template <int D>
@@ -254,27 +281,54 @@ sparse_dq_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k,
   const int32_t* sel = selected + (b * qb + qblk) * topk;
   const float* kbase = k + b * (int64_t)skv * D;
   const float* vbase = v + b * (int64_t)skv * D;
-  for (int s = 0; s < topk; ++s) {
-    const int kv = sel[s];
-    if (kv < 0 || kv >= kb) continue;
-    const int nvb = clamp_valid(kv_vbs[kv], BE);
-    for (int c0 = 0; c0 < nvb; c0 += kChunk) {
-      const int nk = min(kChunk, nvb - c0);
-      __syncthreads();
+  // chunk cursor over the route: slot s, key block kv with nvb valid keys, first key c0
+  auto advance = [&](int& s, int& kv, int& nvb, int& c0) {
+    c0 += kChunk;
+    while (c0 >= nvb) {
+      if (++s >= topk) return false;
+      kv = sel[s];
+      nvb = (kv >= 0 && kv < kb) ? clamp_valid(kv_vbs[kv], BE) : 0;
+      c0 = 0;
+    }
+    return true;
+  };
+  // head_dim <= 128: the next chunk's loads stay in flight under this chunk's
+  // products (64 more registers); head_dim 256 has no registers to spare
+  constexpr bool kPrefetch = D <= 128;
+  Stage32<D, LD, C::NT> kst, vst;
+  auto load_chunk = [&](int kv_, int nvb_, int c0_) {
+    if constexpr (kPrefetch) {
+      kst.load(kbase + ((int64_t)kv_ * BE + c0_) * D, min(kChunk, nvb_ - c0_));
+      vst.load(vbase + ((int64_t)kv_ * BE + c0_) * D, min(kChunk, nvb_ - c0_));
+    }
+  };
+  int s = -1, kv = 0, nvb = 0, c0 = 0;
+  bool have = advance(s, kv, nvb, c0);
+  if (have) load_chunk(kv, nvb, c0);
+  while (have) {
+    const int nk = min(kChunk, nvb - c0);
+    __syncthreads();
+    if constexpr (kPrefetch) {
+      kst.store(ks);
+      vst.store(vs);
+    } else {
       stage32<D, LD, C::NT>(ks, kbase + ((int64_t)kv * BE + c0) * D, nk);
       stage32<D, LD, C::NT>(vs, vbase + ((int64_t)kv * BE + c0) * D, nk);
-      __syncthreads();
-      f32x16 sacc = f32x16{}, pacc = f32x16{};
-      mma_rows<D, LD>(sacc, ks, qf, r, h);
-      mma_rows<D, LD>(pacc, vs, df, r, h);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = 8 * (i >> 2) + 4 * h + (i & 3);
-        const float p = key < nk ? exp2f(fmaf(sacc[i], c2, -my_lse)) : 0.f;
-        sacc[i] = p * (pacc[i] - my_delta);
-      }
-      mma_cols<D, LD>(acc, ks, sacc, r, h);
     }
+    const bool have2 = advance(s, kv, nvb, c0);
+    if (have2) load_chunk(kv, nvb, c0);
+    __syncthreads();
+    f32x16 sacc = f32x16{}, pacc = f32x16{};
+    mma_rows<D, LD>(sacc, ks, qf, r, h);
+    mma_rows<D, LD>(pacc, vs, df, r, h);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = 8 * (i >> 2) + 4 * h + (i & 3);
+      const float p = key < nk ? exp2f(fmaf(sacc[i], c2, -my_lse)) : 0.f;
+      sacc[i] = p * (pacc[i] - my_delta);
+    }
+    mma_cols<D, LD>(acc, ks, sacc, r, h);
+    have = have2;
   }
   float cdiv = 1.f;
   bool cvalid = false;
@@ -340,17 +394,33 @@ sparse_dkdv_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k
   const int32_t* seg = inverse + b * (int64_t)qb * topk + offsets[meta];
   const float* qbase = q + b * (int64_t)sq * D;
   const float* dbase = dout + b * (int64_t)sq * D;
-  for (int e = 0; e < nedge; ++e) {
-    const int qblock = seg[e];
-    for (int c0 = 0; c0 < BE; c0 += kChunk) {
-      const int qrow0 = qblock * BE + c0;
+  // item it: 32 queries (rows (it % (BE/32)) * 32 ..) of in-edge query block it / (BE/32);
+  // head_dim 128: the next item's Q / dO / statistics loads stay in flight
+  // under this item's products (64 more registers; 64 has no headroom at two
+  // waves per SIMD)
+  constexpr int SUBS = BE / kChunk;
+  constexpr bool kPrefetch = D == 128;
+  const int items = nedge * SUBS;
+  Stage32<D, LD, C::NT> qst, ost;
+  float stv = 0.f;  // lse (threads < 32) or delta (32 .. 63) of the staged item
+  auto load_item = [&](int it) {
+    const int qrow0 = seg[it / SUBS] * BE + (it % SUBS) * kChunk;
+    qst.load(qbase + (int64_t)qrow0 * D, kChunk);
+    ost.load(dbase + (int64_t)qrow0 * D, kChunk);
+    if (threadIdx.x < 2 * kChunk)
+      stv = threadIdx.x < kChunk ? lse[b * sq + qrow0 + threadIdx.x]
+                                 : delta[b * sq + qrow0 + threadIdx.x - kChunk];
+  };
+  if (kPrefetch && items > 0) load_item(0);
+  for (int it = 0; it < items; ++it) {
+    {
       __syncthreads();
-      stage32<D, LD, C::NT>(qs, qbase + (int64_t)qrow0 * D, kChunk);
-      stage32<D, LD, C::NT>(os, dbase + (int64_t)qrow0 * D, kChunk);
-      if (threadIdx.x < kChunk) {
-        ls[threadIdx.x] = lse[b * sq + qrow0 + threadIdx.x];
-        es[threadIdx.x] = delta[b * sq + qrow0 + threadIdx.x];
-      }
+      if (!kPrefetch) load_item(it);
+      qst.store(qs);
+      ost.store(os);
+      if (threadIdx.x < kChunk) ls[threadIdx.x] = stv;
+      else if (threadIdx.x < 2 * kChunk) es[threadIdx.x - kChunk] = stv;
+      if (kPrefetch && it + 1 < items) load_item(it + 1);
       __syncthreads();
       f32x16 sacc = f32x16{}, pacc = f32x16{};
       mma_rows<D, LD>(sacc, qs, kf, r, h);   // S  (queries x keys), lane column = key r
