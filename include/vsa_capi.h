@@ -168,15 +168,19 @@ int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, const void* d
                       float scale, int32_t dtype, void* stream);
 
 /*
- * Dispatch order for vsa_sparse_bwd_dkdv's bf16 / fp16 workgroups, from the
+ * Scheduling workspace for vsa_sparse_bwd_dkdv's bf16 / fp16 kernel, from the
  * CSR counts of vsa_csr_build.  No reference counterpart: the reference's
  * dK/dV launch walks key blocks in index order (triton_impl.py:1394-1440), and
  * a hot key block (in-edges from most query blocks, as with skewed routes)
- * then serialises the end of the kernel.  The grid's XCD ranges are listed
- * longest-first when their largest tile exceeds a quarter of an average
- * workgroup slot's share, else in order.  tile_order holds order_len >=
- * 8 * ceil(tiles / 8) int32 entries, tiles = bh * skv / min(block_elements,
- * 128) * (head_dim > 128 ? 2 : 1).  Results do not depend on the order.
+ * then serialises the end of the kernel.  The kernel's persistent workgroups
+ * take the tiles of their XCD's range in the order written here: longest-first
+ * when the range's largest tile exceeds a quarter of an average workgroup
+ * slot's share, else index order.  tile_order holds order_len >= 8 * per + 16
+ * int32 entries, per = ceil(tiles / 8), tiles = bh * skv / min(block_elements,
+ * 128) * (head_dim > 128 ? 2 : 1): the order, then 9 counters this call zeroes
+ * and the dK/dV kernel advances (and leaves zeroed when it ends), so one
+ * workspace serves one dK/dV launch at a time.  Results do not depend on the
+ * order.
  */
 int vsa_dkdv_tile_order(const int32_t* counts, int32_t* tile_order, int64_t order_len,
                         int64_t bh, int64_t skv, int32_t head_dim, int32_t block_elements,
@@ -186,9 +190,10 @@ int vsa_dkdv_tile_order(const int32_t* counts, int32_t* tile_order, int64_t orde
  * KV-owned dK/dV driven by the CSR from vsa_csr_build.  Replaces
  * _vsa_dkdv_256_kernel / _vsa_dkdv_kernel (triton_impl.py:972-1318).  When
  * d_k_c / d_v_c != NULL the pooled gradients are folded in as in
- * vsa_sparse_bwd_dq (using kv_vbs).  tile_order (nullable) is the dispatch
- * order from vsa_dkdv_tile_order for the same sizes (bf16 / fp16; ignored
- * for fp32).
+ * vsa_sparse_bwd_dq (using kv_vbs).  tile_order (nullable) is the workspace
+ * from vsa_dkdv_tile_order for the same sizes (bf16 / fp16; ignored for
+ * fp32); without it the persistent workgroups stride over the tiles in index
+ * order.
  */
 int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
                         const float* lse, const float* delta, const int32_t* counts,
@@ -197,7 +202,7 @@ int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v, const void*
                         const void* d_k_c, const void* d_v_c,
                         int64_t bh, int64_t sq, int64_t skv, int32_t head_dim,
                         int32_t block_elements, int32_t topk, float scale,
-                        const int32_t* tile_order, int32_t dtype, void* stream);
+                        int32_t* tile_order, int32_t dtype, void* stream);
 
 /*
  * Tile-layout metadata for a (T, H, W) latent grid and (ts, hs, ws) tiles, in

@@ -240,27 +240,34 @@ struct DkvCfg {
 };
 
 template <typename T, int D, int BE>
-__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_dkdv_kernel(
+struct DkvShared {
+  using C = DkvCfg<D, BE>;
+  __attribute__((aligned(16))) T smem[C::NS][2 * C::TILE];
+  __attribute__((aligned(16))) float sstat[C::NS][2][C::QS];  // [stage][lse, delta][query]
+  int32_t sseg[C::SEGMAX];
+};
+
+// One key tile (tile_s < num_tiles) of sparse_dkdv_kernel, start to finish.
+// On return every wave's direct loads may still be in flight (the last steps
+// re-copy the last item): the caller drains them before the LDS is reused.
+template <typename T, int D, int BE>
+__device__ __forceinline__ void dkdv_tile(
+    DkvShared<T, D, BE>& sh, int tile_s,
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ inverse, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ dk, T* __restrict__ dv, const T* __restrict__ dkc,
-    const T* __restrict__ dvc, int num_tiles, int tiles_per_head, int sq, int skv, int qb,
-    int kb, int topk, float c2, uint32_t ksign, float scale,
-    const int32_t* __restrict__ tile_order) {
+    const T* __restrict__ dvc, int tiles_per_head, int sq, int skv, int qb,
+    int kb, int topk, float c2, uint32_t ksign, float scale) {
   using C = DkvCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
   constexpr int NS = C::NS, NA = C::NA, NC = C::NC, L = C::L, TP = C::TP;
-  __shared__ __attribute__((aligned(16))) T smem[NS][2 * C::TILE];
-  __shared__ __attribute__((aligned(16))) float sstat[NS][2][C::QS];  // [stage][lse, delta][query]
-  __shared__ int32_t sseg[C::SEGMAX];
+  auto& smem = sh.smem;
+  auto& sstat = sh.sstat;
+  auto& sseg = sh.sseg;
 
-  // workgroup i runs on XCD i % 8; tile_order (from dkdv_order_kernel) permutes
-  // each XCD's contiguous tile range, else the range is walked in order
-  const int tile_s = tile_order ? tile_order[blockIdx.x] : xcd_tile(blockIdx.x, num_tiles);
-  if (tile_s >= num_tiles) return;
   const int tile = tile_s / C::NSPLIT;
   const int d_off = (tile_s % C::NSPLIT) * C::DH;  // first dK/dV dim of this workgroup
   const int64_t b = tile / tiles_per_head;
@@ -566,6 +573,56 @@ epilogue:
   }
 }
 
+// Persistent dK/dV: as many workgroups as the CUs hold at once, each looping
+// over key tiles (a workgroup per tile left every CU idle between one tile's
+// end and the next one's start, about 5 % of the kernel, plus an uneven tail).
+// Workgroup i runs on XCD i % 8 and takes tiles from that XCD's contiguous
+// range: with a tile_order workspace (vsa_dkdv_tile_order) the next entry of
+// the range's order comes from the XCD's counter (so early finishers take more
+// tiles) and the last workgroup to finish zeroes the counters for the next
+// launch; without one, a fixed stride over the range in index order.
+template <typename T, int D, int BE>
+__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_dkdv_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ inverse, const int32_t* __restrict__ kv_vbs,
+    T* __restrict__ dk, T* __restrict__ dv, const T* __restrict__ dkc,
+    const T* __restrict__ dvc, int num_tiles, int tiles_per_head, int sq, int skv, int qb,
+    int kb, int topk, float c2, uint32_t ksign, float scale, int32_t* __restrict__ tile_order) {
+  __shared__ DkvShared<T, D, BE> sh;
+  __shared__ int s_next;
+  const int xcd = blockIdx.x & 7;
+  const int per = (num_tiles + 7) >> 3;       // tiles per XCD range
+  const int stride = (int)(gridDim.x >> 3);   // workgroups per XCD
+  int32_t* ctr = tile_order ? tile_order + 8 * per : nullptr;  // [8 ranges][done]
+  for (int round = 0;; ++round) {
+    int j;
+    if (ctr) {
+      if (threadIdx.x == 0) s_next = atomicAdd(ctr + xcd, 1);
+      __syncthreads();
+      j = s_next;
+    } else {
+      j = (int)(blockIdx.x >> 3) + round * stride;
+    }
+    if (j >= per) break;
+    const int tile_s = ctr ? tile_order[xcd + 8 * j] : xcd * per + j;
+    if (tile_s < num_tiles)
+      dkdv_tile<T, D, BE>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets, inverse,
+                          kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb, kb, topk, c2,
+                          ksign, scale);
+    dma_wait();       // this wave's trailing copies land before the LDS is reused
+    __syncthreads();  // and every wave is done with it (and with s_next)
+  }
+  if (ctr && threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(ctr + 8, 1) == (int)gridDim.x - 1) {
+#pragma unroll
+      for (int x = 0; x < 9; ++x) ctr[x] = 0;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Ping-pong dQ for 256-token blocks: the schedule of the 8-wave forward.
 // One workgroup of 8 waves owns a query block; group 0 (waves 0-3) and group 1
@@ -800,6 +857,21 @@ sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
   dq_epilogue<T, D, BE>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale);
 }
 
+// CUs of the current device (cached per device; a racy first fill writes the
+// same value)
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <typename T, int D>
 static int launch_dq_pp(const void* q, const void* k, const void* v, const void* dout,
                         const float* lse, const float* delta, const int32_t* selected,
@@ -841,13 +913,17 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
                        const float* lse, const float* delta, const int32_t* counts,
                        const int32_t* offsets, const int32_t* inverse, const int32_t* kv_vbs,
                        void* dk, void* dv, const void* dkc, const void* dvc, int64_t bh,
-                       int64_t sq, int64_t skv, int topk, float scale, const int32_t* tile_order,
+                       int64_t sq, int64_t skv, int topk, float scale, int32_t* tile_order,
                        hipStream_t stream) {
   using C = DkvCfg<D, BE>;
   const int tph = (int)(skv / C::KT);
   const int64_t tiles = bh * tph * C::NSPLIT;
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
-  const int grid = (int)(((tiles + 7) / 8) * 8);
+  // persistent: the workgroups the CUs hold at once (one wave per SIMD), at
+  // most one per tile, a multiple of 8 (the XCD count)
+  const int resident = cu_count() * (4 / C::NW);
+  const int64_t want = ((tiles + 7) / 8) * 8;
+  const int grid = (int)(want < resident ? want : (resident / 8) * 8);
   hipLaunchKernelGGL((sparse_dkdv_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, counts,
                      offsets, inverse, kv_vbs, (T*)dk, (T*)dv, (const T*)dkc, (const T*)dvc,
@@ -882,6 +958,10 @@ __global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restr
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int x = blockIdx.x;
   const int lo = x * per, n = max(0, min(per, num_tiles - lo));
+  // the scheduling counters sparse_dkdv_kernel advances: one per range, then
+  // the finished-workgroup count
+  if (tid == 0) order[8 * per + x] = 0;
+  if (tid == 0 && x == 0) order[8 * per + 8] = 0;
   auto nedge_of = [&](int j) {
     const int tile = (lo + j) / nsplit;
     return counts[(int64_t)(tile / tph) * kb + (tile % tph) / tpb];
@@ -1004,7 +1084,7 @@ extern "C" int vsa_dkdv_tile_order(const int32_t* counts, int32_t* tile_order,
   if (!dkdv_geometry(D, be, skv, g)) return VSA_ERR_UNSUPPORTED;
   const int64_t tiles = bh * g.tph * g.nsplit;
   const int64_t per = (tiles + 7) / 8;
-  if (tiles > (1LL << 30) || order_len < 8 * per) return VSA_ERR_SHAPE;
+  if (tiles > (1LL << 30) || order_len < 8 * per + 16) return VSA_ERR_SHAPE;
   hipLaunchKernelGGL(dkdv_order_kernel, dim3(8), dim3(1024), 0, (hipStream_t)stream, counts,
                      tile_order, (int)tiles, (int)per, g.tph, g.tpb, g.nsplit,
                      (int)(skv / be), 32 * g.wg_per_cu);
@@ -1017,7 +1097,7 @@ extern "C" int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v,
                                    const int32_t* inverse, const int32_t* kv_vbs, void* dk,
                                    void* dv, const void* d_k_c, const void* d_v_c, int64_t bh,
                                    int64_t sq, int64_t skv, int32_t D, int32_t be, int32_t topk,
-                                   float scale, const int32_t* tile_order, int32_t dtype,
+                                   float scale, int32_t* tile_order, int32_t dtype,
                                    void* stream) {
   if (!q || !k || !v || !dout || !lse || !delta || !counts || !offsets || !inverse || !kv_vbs ||
       !dk || !dv)

@@ -340,12 +340,13 @@ def sparse_backward(q, k, v, dout, lse, delta, selected, variable_block_sizes, b
 
 
 def dkdv_tile_order(counts, bh, skv, head_dim, block_elements):
-    """Dispatch order of the bf16/fp16 dK/dV workgroups: each XCD's tile range
-    longest-first when one key block's in-edge count would otherwise set the
-    kernel's end (skewed routes), else in order (see vsa_dkdv_tile_order)."""
+    """Scheduling workspace of the bf16/fp16 dK/dV kernel: each XCD's tile
+    range longest-first when one key block's in-edge count would otherwise set
+    the kernel's end (skewed routes), else in order, followed by the counters
+    the persistent workgroups take tiles from (see vsa_dkdv_tile_order)."""
     kt = 128 if block_elements >= 128 else block_elements
     tiles = bh * (skv // kt) * (2 if head_dim > 128 else 1)
-    order = torch.empty(8 * ((tiles + 7) // 8), device=counts.device, dtype=torch.int32)
+    order = torch.empty(8 * ((tiles + 7) // 8) + 16, device=counts.device, dtype=torch.int32)
     _lib.call("vsa_dkdv_tile_order", _lib.ptr(counts), _lib.ptr(order), order.numel(), bh, skv,
               head_dim, block_elements, _lib.stream_of(counts))
     return order

@@ -53,9 +53,9 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     p = _lib.ptr(torch.zeros(1))
     assert lib.vsa_topk(p, p, 1, 4, 5, None) == -2          # topk > Kb
     assert lib.vsa_csr_build(p, p, p, p, 1, 4, 0, 2, None) == -2
-    # tile order: the buffer must hold 8 * ceil(tiles / 8) entries
-    assert lib.vsa_dkdv_tile_order(None, p, 8, 1, 1024, 128, 256, None) == -1
-    assert lib.vsa_dkdv_tile_order(p, p, 7, 1, 1024, 128, 256, None) == -2    # 8 tiles
+    # tile order: the buffer must hold 8 * ceil(tiles / 8) + 16 entries
+    assert lib.vsa_dkdv_tile_order(None, p, 24, 1, 1024, 128, 256, None) == -1
+    assert lib.vsa_dkdv_tile_order(p, p, 23, 1, 1024, 128, 256, None) == -2   # 8 tiles
     assert lib.vsa_dkdv_tile_order(p, p, 64, 1, 1024, 128, 96, None) == -2   # 1024 % 96
     assert lib.vsa_dkdv_tile_order(p, p, 64, 1, 960, 128, 96, None) == -4    # no kernel
     assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,

@@ -95,11 +95,13 @@ def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
     kt = 128 if be >= 128 else be
     nsplit = 2 if D > 128 else 1
     tiles = H * (S // kt) * nsplit
-    o = order.cpu().numpy()
+    per = (tiles + 7) // 8
+    assert order.numel() == 8 * per + 16
+    assert (order[8 * per:8 * per + 9] == 0).all()           # scheduling counters, reset
+    o = order[:8 * per].cpu().numpy()
     real = o[o < tiles]
     assert sorted(real.tolist()) == list(range(tiles))        # every tile exactly once
     assert (o[o >= tiles] == tiles).all()                     # the rest are the sentinel
-    per = (tiles + 7) // 8
     nedge = cnt.cpu().reshape(H, nb).repeat_interleave(be // kt, 1).reshape(-1)
     nedge = nedge.repeat_interleave(nsplit)
     slots = 32 * (4 // (kt // 32))                            # concurrent workgroups per XCD
@@ -128,3 +130,4 @@ def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
     torch.cuda.synchronize()
     for a, b_ in zip(*res):
         assert torch.equal(a, b_)
+    assert (order[8 * per:8 * per + 9] == 0).all()           # left reset for the next launch
