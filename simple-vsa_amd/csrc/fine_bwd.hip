@@ -643,26 +643,28 @@ struct DqPPCfg {
   static constexpr int NS = 4;
 };
 
+// One query block (tile < bh * Sq / 256) of sparse_dq_pp_kernel.
 template <typename T, int D>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
-sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-                    const T* __restrict__ dout, const float* __restrict__ lse,
-                    const float* __restrict__ delta, const int32_t* __restrict__ selected,
-                    const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
-                    const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
-                    int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
-                    float scale) {
+__device__ __forceinline__ void dq_pp_tile(
+    T* smem, int tile, const T* __restrict__ q, const T* __restrict__ k,
+    const T* __restrict__ v, const T* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ delta, const int32_t* __restrict__ selected,
+    const int32_t* __restrict__ kv_vbs, T* __restrict__ dq, const T* __restrict__ dqc,
+    const int32_t* __restrict__ q_vbs, int sq, int skv, int qb, int kb, int topk, float c2,
+    uint32_t qsign, float scale) {
   constexpr int BE = 256;
   using C = DqPPCfg<D>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
-  __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
 
-  const int tile = xcd_tile(blockIdx.x, num_tiles);
-  if (tile >= num_tiles) return;
   const int64_t b = tile / qb;
   const int qblk = tile % qb;
-  const int tid = threadIdx.x, lane = tid & 63;
+  // the lane index passes through an asm that reads the tile, so the lane
+  // offsets derived from it are recomputed per tile in the persistent loop
+  // instead of being hoisted out of it and kept (spilled) across the tile
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid) : "s"(tile));
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   const bool grp1 = wave >= 4;
@@ -857,19 +859,27 @@ sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
   dq_epilogue<T, D, BE>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale);
 }
 
-// CUs of the current device (cached per device; a racy first fill writes the
-// same value)
-static int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
+// Persistent, with the query-block walk of sparse_fwd_pp_kernel.
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+                    const T* __restrict__ dout, const float* __restrict__ lse,
+                    const float* __restrict__ delta, const int32_t* __restrict__ selected,
+                    const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
+                    const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
+                    int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
+                    float scale) {
+  using C = DqPPCfg<D>;
+  __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
+  const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
+  for (int j = (int)(blockIdx.x >> 3); j < per; j += stride) {
+    const int tile = xcd * per + j;
+    if (tile >= num_tiles) break;
+    dq_pp_tile<T, D>(smem, tile, q, k, v, dout, lse, delta, selected, kv_vbs, dq, dqc, q_vbs, sq,
+                     skv, qb, kb, topk, c2, qsign, scale);
+    dma_wait();
+    __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
   }
-  return cached[dev];
 }
 
 template <typename T, int D>
@@ -880,7 +890,9 @@ static int launch_dq_pp(const void* q, const void* k, const void* v, const void*
                         hipStream_t stream) {
   const int64_t tiles = bh * (sq / 256);
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
-  const int grid = (int)(((tiles + 7) / 8) * 8);
+  const int64_t want = ((tiles + 7) / 8) * 8;
+  const int resident = (cu_count() / 8) * 8;  // one 8-wave workgroup per CU
+  const int grid = (int)(want < resident ? want : resident);
   hipLaunchKernelGGL((sparse_dq_pp_kernel<T, D>), dim3(grid), dim3(512), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, selected,
                      kv_vbs, (T*)dq, (const T*)dqc, q_vbs, (int)tiles, (int)sq, (int)skv,

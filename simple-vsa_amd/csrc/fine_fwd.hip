@@ -279,24 +279,27 @@ struct FwdPPCfg {
   static constexpr int PER = 2 * (KC * D / 8 / NT);  // direct loads per wave per chunk
 };
 
+// One query block (tile < bh * Sq / 256) of sparse_fwd_pp_kernel.
 template <typename T, int D>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
-sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-                     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
-                     T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
-                     const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles,
-                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
+__device__ __forceinline__ void fwd_pp_tile(
+    T* smem, int tile, const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
+    T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
+    const T* __restrict__ gate, int gate_mode, int gate_heads, int sq, int skv, int qb, int kb,
+    int topk, float c2, uint32_t qsign) {
   constexpr int BE = 256;
   using C = FwdPPCfg<D>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
-  __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
 
-  const int tile = xcd_tile(blockIdx.x, num_tiles);
-  if (tile >= num_tiles) return;
   const int64_t b = tile / qb;
   const int qblk = tile % qb;
-  const int tid = threadIdx.x, lane = tid & 63;
+  // the lane index passes through an asm that reads the tile, so the lane
+  // offsets derived from it are recomputed per tile in the persistent loop
+  // instead of being hoisted out of it and kept (spilled) across the tile
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid) : "s"(tile));
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: group branches are scalar
   const int r = lane & 31, h = lane >> 5;
   const bool grp1 = wave >= 4;
@@ -563,6 +566,30 @@ sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
                      gate_heads);
 }
 
+// Persistent: as many workgroups as the CUs hold (one each), every query block
+// has the same topk chunks, so a fixed stride balances them.  Workgroup i runs
+// on XCD i % 8 and walks that XCD's contiguous range of query blocks (the
+// xcd_tile order), so one head's K/V stay in one XCD's L2.
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+                     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
+                     T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
+                     const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles,
+                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
+  using C = FwdPPCfg<D>;
+  __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
+  const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
+  for (int j = (int)(blockIdx.x >> 3); j < per; j += stride) {
+    const int tile = xcd * per + j;
+    if (tile >= num_tiles) break;
+    fwd_pp_tile<T, D>(smem, tile, q, k, v, selected, kv_vbs, out, lse, outc, gate, gate_mode,
+                      gate_heads, sq, skv, qb, kb, topk, c2, qsign);
+    dma_wait();
+    __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
+  }
+}
+
 template <typename T, int D>
 static int launch_fwd_pp(const void* q, const void* k, const void* v, const int32_t* selected,
                          const int32_t* kv_vbs, void* out, float* lse, const void* outc,
@@ -570,7 +597,9 @@ static int launch_fwd_pp(const void* q, const void* k, const void* v, const int3
                          int64_t skv, int topk, float scale, hipStream_t stream) {
   const int64_t tiles = bh * (sq / 256);
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
-  const int grid = (int)(((tiles + 7) / 8) * 8);
+  const int64_t want = ((tiles + 7) / 8) * 8;
+  const int resident = (cu_count() / 8) * 8;  // one 8-wave workgroup per CU
+  const int grid = (int)(want < resident ? want : resident);
   const float c2 = fabsf(scale) * kLog2e;
   const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
   hipLaunchKernelGGL((sparse_fwd_pp_kernel<T, D>), dim3(grid), dim3(512), 0, stream,

@@ -40,3 +40,18 @@
 static inline int vsa_check_launch() {
   return hipGetLastError() == hipSuccess ? VSA_OK : VSA_ERR_LAUNCH;
 }
+
+// CUs of the current device (cached per device; a racy first fill writes the
+// same value)
+static inline int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
