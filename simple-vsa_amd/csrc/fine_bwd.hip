@@ -580,7 +580,8 @@ epilogue:
 // range: with a tile_order workspace (vsa_dkdv_tile_order) the next entry of
 // the range's order comes from the XCD's counter (so early finishers take more
 // tiles) and the last workgroup to finish zeroes the counters for the next
-// launch; without one, a fixed stride over the range in index order.
+// launch; without one, a fixed stride over the range in index order.  Head
+// dim 256 keeps one workgroup per tile (tile_order[i] or the XCD order).
 template <typename T, int D, int BE>
 __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -591,6 +592,16 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     const T* __restrict__ dvc, int num_tiles, int tiles_per_head, int sq, int skv, int qb,
     int kb, int topk, float c2, uint32_t ksign, float scale, int32_t* __restrict__ tile_order) {
   __shared__ DkvShared<T, D, BE> sh;
+  if constexpr (DkvCfg<D, BE>::NSPLIT > 1) {
+    // head_dim 256: one tile per workgroup (the loop's state would push the
+    // fragments and accumulators, which fill the register file, into scratch)
+    const int tile_s = tile_order ? tile_order[blockIdx.x] : xcd_tile(blockIdx.x, num_tiles);
+    if (tile_s < num_tiles)
+      dkdv_tile<T, D, BE>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets, inverse,
+                          kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb, kb, topk, c2,
+                          ksign, scale);
+    return;
+  }
   __shared__ int s_next;
   const int xcd = blockIdx.x & 7;
   const int per = (num_tiles + 7) >> 3;       // tiles per XCD range
@@ -935,7 +946,7 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
   // most one per tile, a multiple of 8 (the XCD count)
   const int resident = cu_count() * (4 / C::NW);
   const int64_t want = ((tiles + 7) / 8) * 8;
-  const int grid = (int)(want < resident ? want : (resident / 8) * 8);
+  const int grid = C::NSPLIT > 1 || want < resident ? (int)want : (resident / 8) * 8;
   hipLaunchKernelGGL((sparse_dkdv_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, counts,
                      offsets, inverse, kv_vbs, (T*)dk, (T*)dv, (const T*)dkc, (const T*)dvc,
