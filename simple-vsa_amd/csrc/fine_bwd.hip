@@ -378,11 +378,16 @@ __device__ __forceinline__ void dkdv_tile(
     }
   };
 
+  // Each accumulator leaves its zero through an asm of its own: without it the
+  // compiler shares one zero register between them and the S / dP tiles and
+  // then moves two dK/dV accumulators aside every step to make room for S/dP
+  // (about 16 extra accumulator moves per step, and a spill at head_dim 256).
   f32x16 dkacc[C::DH / 32], dvacc[C::DH / 32];
 #pragma unroll
   for (int mt = 0; mt < C::DH / 32; ++mt) {
     dkacc[mt] = f32x16{};
     dvacc[mt] = f32x16{};
+    asm volatile("" : "+a"(dkacc[mt]), "+a"(dvacc[mt]));
   }
 
   auto row_read = [&](int stg, int tilesel, int ks) {

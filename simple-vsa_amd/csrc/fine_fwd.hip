@@ -435,7 +435,7 @@ __device__ __forceinline__ void fwd_pp_tile(
     if (st >= 4) {
       const float negm = -m;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) tv[(st - 4) * 8 + i] = fmaf(tv[(st - 4) * 8 + i], c2, negm);
+      for (int i = 0; i < 8; ++i) tv[(st - 4) * 8 + i] = here(fmaf(tv[(st - 4) * 8 + i], c2, negm));
     }
   };
   auto finish = [&](int nv) {

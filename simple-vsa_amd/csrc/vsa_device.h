@@ -241,6 +241,14 @@ __device__ __forceinline__ X opaque(X x) {
   return x;
 }
 
+// Compute a value at this program point: the compiler sinks arithmetic whose
+// only use sits in a later conditional block into that block, which would
+// move work scheduled under one phase's MFMAs into the next phase.
+__device__ __forceinline__ float here(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
