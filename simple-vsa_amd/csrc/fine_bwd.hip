@@ -764,8 +764,9 @@ __device__ __forceinline__ void dq_pp_tile(
   // MFMA phase: when with_dq, dQ += K_{j-1}^T dS_{j-1}^T first (16 MFMAs, K^T
   // of stage sp; the packed dS dies before S and dP are written), then S_j and
   // dP_j (32 MFMAs, K and V rows of stage sj); every LDS operand is read L
-  // MFMAs ahead of its use.
-  constexpr int NSP = 4 * (D / 16), NDQ = 4 * (D / 32), L = 2;
+  // MFMAs ahead of its use (head_dim 128: 2, the most that does not spill
+  // inside the chunk loop).
+  constexpr int NSP = 4 * (D / 16), NDQ = 4 * (D / 32), L = D == 128 ? 2 : 8;
   auto mma_x = [&](int sj, int sp, auto with_dq) {
     constexpr int N0 = decltype(with_dq)::value ? NDQ : 0;  // dQ products first
     constexpr int NX = N0 + NSP;
