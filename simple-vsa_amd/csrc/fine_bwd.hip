@@ -57,6 +57,7 @@ __device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64
     cdiv = (float)(cnt > 1 ? cnt : 1);
     crow = dqc + ((int64_t)b * qb + qblk) * D;
   }
+  const float rcp = 1.0f / cdiv;
   u32x2 cr[D / 32][4];  // loaded together, so their latency is paid once
   if (cvalid) {
 #pragma unroll
@@ -74,7 +75,7 @@ __device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64
       if (cvalid) {
         const T* cc = reinterpret_cast<const T*>(&cr[mt][g]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) cval[e] = round_t<T>(E::to_f(cc[e]) / cdiv);
+        for (int e = 0; e < 4; ++e) cval[e] = round_t<T>(div_by_count(E::to_f(cc[e]), cdiv, rcp));
       }
       T o4[4];
 #pragma unroll
@@ -542,9 +543,23 @@ __device__ __forceinline__ void dkdv_tile(
 epilogue:
   // ---- epilogue ------------------------------------------------------------
   const int32_t cnt = kv_vbs[kvblk];
-  const float cdiv = (float)(cnt > 1 ? cnt : 1);
+  const float cdiv = (float)(cnt > 1 ? cnt : 1), rcp = 1.0f / cdiv;
   const T* kcrow = dkc ? dkc + ((int64_t)b * kb + kvblk) * D : nullptr;
   const T* vcrow = dvc ? dvc + ((int64_t)b * kb + kvblk) * D : nullptr;
+  // The pooled-gradient rows are loaded together before the first store: a
+  // load issued after a store waits for that store too (one in-order vector
+  // memory counter), which made the epilogue 16 store round trips long.
+  u32x2 kcv[C::DH / 32][4], vcv[C::DH / 32][4];
+  if (key_valid && kcrow) {
+#pragma unroll
+    for (int mt = 0; mt < C::DH / 32; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = d_off + mt * 32 + 8 * g + 4 * h;
+        kcv[mt][g] = *reinterpret_cast<const u32x2*>(kcrow + d0);
+        vcv[mt][g] = *reinterpret_cast<const u32x2*>(vcrow + d0);
+      }
+  }
 #pragma unroll
   for (int mt = 0; mt < C::DH / 32; ++mt) {
 #pragma unroll
@@ -552,14 +567,12 @@ epilogue:
       const int d0 = d_off + mt * 32 + 8 * g + 4 * h;
       float ck[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
       if (key_valid && kcrow) {
-        u32x2 a = *reinterpret_cast<const u32x2*>(kcrow + d0);
-        u32x2 bb = *reinterpret_cast<const u32x2*>(vcrow + d0);
-        const T* ka = reinterpret_cast<const T*>(&a);
-        const T* va = reinterpret_cast<const T*>(&bb);
+        const T* ka = reinterpret_cast<const T*>(&kcv[mt][g]);
+        const T* va = reinterpret_cast<const T*>(&vcv[mt][g]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          ck[e] = round_t<T>(E::to_f(ka[e]) / cdiv);
-          cv[e] = round_t<T>(E::to_f(va[e]) / cdiv);
+          ck[e] = round_t<T>(div_by_count(E::to_f(ka[e]), cdiv, rcp));
+          cv[e] = round_t<T>(div_by_count(E::to_f(va[e]), cdiv, rcp));
         }
       }
       // A padding key gets no gradient; its lane's accumulators (which only
