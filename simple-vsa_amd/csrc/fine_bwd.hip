@@ -278,7 +278,8 @@ __device__ __forceinline__ void dkdv_tile(
   const int r = lane & 31, h = lane >> 5;
   const int mykey = k0 + wave * 32 + r;
   const int64_t ktok = (int64_t)b * skv + mykey;
-  const int nvb = clamp_valid(kv_vbs[kvblk], BE);
+  const int32_t cnt = kv_vbs[kvblk];  // read once: the epilogue's pooled division needs it too
+  const int nvb = clamp_valid(cnt, BE);
   const bool key_valid = (mykey - kvblk * BE) < nvb;
 
   // K^T, V^T fragments (B operands): lane (r, h) holds key r, dims 16ks + 8h ..
@@ -542,7 +543,6 @@ __device__ __forceinline__ void dkdv_tile(
 
 epilogue:
   // ---- epilogue ------------------------------------------------------------
-  const int32_t cnt = kv_vbs[kvblk];
   const float cdiv = (float)(cnt > 1 ? cnt : 1), rcp = 1.0f / cdiv;
   const T* kcrow = dkc ? dkc + ((int64_t)b * kb + kvblk) * D : nullptr;
   const T* vcrow = dvc ? dvc + ((int64_t)b * kb + kvblk) * D : nullptr;
