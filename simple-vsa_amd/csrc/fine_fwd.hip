@@ -58,7 +58,6 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
   const float ltot = pair_sum32(lsum);
   const float inv = 1.0f / ltot;
   const int64_t tok = (int64_t)b * sq + myq;
-  if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
   const T* ocrow = outc ? outc + ((int64_t)b * qb + qblk) * D : nullptr;
   float gtok = 1.f;
   if (outc && gate_mode == 2) gtok = E::to_f(gate[tok]);
@@ -108,6 +107,8 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
       *reinterpret_cast<u32x2*>(out + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
     }
   }
+  // stored last: a load issued after a store also waits for that store
+  if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
 }
 
 template <typename T, int D, int BE>
