@@ -443,16 +443,27 @@ sparse_dkdv_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k
   }
   const int32_t cnt = kv_vbs[kvblk];
   const float cdiv = (float)(cnt > 1 ? cnt : 1);
+  // pooled-gradient rows loaded before the first store (a load issued after a
+  // store also waits for that store)
+  f32x4 ckr[D / 32][4], cvr[D / 32][4];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      ckr[mt][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      cvr[mt][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (key_valid && dkc) {
+        const int d0 = 32 * mt + 8 * g + 4 * h;
+        ckr[mt][g] = *reinterpret_cast<const f32x4*>(dkc + meta * D + d0);
+        cvr[mt][g] = *reinterpret_cast<const f32x4*>(dvc + meta * D + d0);
+      }
+    }
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * mt + 8 * g + 4 * h;
-      f32x4 ck = {0.f, 0.f, 0.f, 0.f}, cv = {0.f, 0.f, 0.f, 0.f};
-      if (key_valid && dkc) {
-        ck = *reinterpret_cast<const f32x4*>(dkc + meta * D + d0);
-        cv = *reinterpret_cast<const f32x4*>(dvc + meta * D + d0);
-      }
+      const f32x4 ck = ckr[mt][g], cv = cvr[mt][g];
       f32x4 kk, vv;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
