@@ -338,6 +338,18 @@ def test_full_vsa_padding_and_gate_be64(dtype):
     _full_vsa_case(dtype, 64, 128, 2, [64, 41, 64, 19], 2, "full", 31)
 
 
+@pytest.mark.parametrize("be,d", [(256, 128), (64, 64)])
+def test_full_vsa_unselected_key_blocks_get_compression_gradient(be, d):
+    # tests/test_torch_vsa.py:89-109 on the GPU: with topk 1 most key blocks
+    # have no CSR in-edge, so their dK/dV tiles run no item and carry only the
+    # pooled (compression-branch) gradient, folded in the dK/dV epilogue
+    vbs = [be] * 9
+    vbs[4] = be - 29          # a ragged block: the pooled division is not by a power of two
+    sel = _full_vsa_case(torch.bfloat16, be, d, 2, vbs, 1, None, 41)
+    unselected = [len(vbs) - len(set(sel[0, h].flatten().tolist())) for h in range(sel.shape[1])]
+    assert all(n > 0 for n in unselected), f"the case must leave key blocks unselected: {unselected}"
+
+
 def test_full_vsa_be256_padded_no_gate():
     _full_vsa_case(torch.bfloat16, 256, 128, 1, [256, 173], 2, None, 35)
 
