@@ -3,7 +3,7 @@
 Workload (the metric's configuration): fused VSA
 forward + backward, B=1, H=40, S=40,960, D=128, bf16, block (4,8,8) -> 256
 tokens, 160 full blocks, topk=20, gate ~ U(0,1) of shape [B,H,S,D];
-q, k, v, dO ~ N(0,1).  A step is one forward + backward of ``vsa.mi355x_vsa``
+q, k, v, dO ~ N(0,1).  A step is one forward + backward of ``vsa_mi355x.mi355x_vsa``
 over that synthetic batch, inputs resident in HBM.
 
 value = effective TFLOP/s = 3.5 * 4*B*H*Qb*topk*be^2*D / step time (only the
@@ -116,7 +116,7 @@ def run_workload(key, steps, warmup):
     """Time fwd and fwd+bwd of one BASELINE workload; report ms, effective
     TFLOP/s and the peak HBM the op allocates beyond its inputs."""
     import torch
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     w = WORKLOADS[key]
     dev = torch.device("cuda", 0)
     B, H, S, D, topk = w["B"], w["H"], w["S"], w["D"], w["topk"]
@@ -184,7 +184,7 @@ def run_tiling(steps, warmup):
     20 x 32 x 64 latent in (4, 8, 8) tiles) and of a latent with partial tiles;
     HBM-bound row moves, reported against the 8 TB/s roof (read + write bytes)."""
     import torch
-    from vsa import tiling
+    from vsa_mi355x import tiling
     out = {"workload": "tiling", "cases": []}
     for shape, ts, inner in (((20, 32, 64), (4, 8, 8), (40, 128)),
                              ((21, 30, 52), (4, 4, 4), (40, 128))):
@@ -221,8 +221,8 @@ def run_gate(steps, warmup):
     gate consumed in the producer's token-major layout, against the same step
     with the gate made contiguous first (what a [B,H,S,D]-only op needs)."""
     import torch
-    from vsa import CompressionGate
-    from vsa import mi355x as M
+    from vsa_mi355x import CompressionGate
+    from vsa_mi355x import mi355x as M
     B, H, S, D, topk = CFG["B"], CFG["H"], CFG["S"], CFG["D"], CFG["topk"]
     be = math.prod(CFG["block"])
     dev = torch.device("cuda", 0)
@@ -279,7 +279,7 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * src.element_size()}))
         return
 
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
 
     if args.workload == "gate":
         print(json.dumps(run_gate(args.steps, args.warmup)), flush=True)
@@ -330,12 +330,12 @@ def main():
         qd, kd, vd, gd = (t.detach() for t in (q, k, v, gate))
         qc, kc, vc = M.block_mean_qkv(qd, kd, vd, vbs, vbs, be)
         _, probs, outc, sel = M.coarse_forward(qc, kc, vc, topk, scale)
-        out, lse = M.sparse_forward(qd, kd, vd, sel, vbs, be, scale, out_c=outc, gate=gd)
-        delta, d_outc, _ = M.backward_prep(out, do, be, out_c=outc, gate=gd)
+        out, lse, fine = M.sparse_forward(qd, kd, vd, sel, vbs, be, scale, out_c=outc, gate=gd)
+        delta, d_outc, _ = M.backward_prep(fine, do, be, out_c=outc, gate=gd)
         dqc, dkc, dvc = M.coarse_backward(qc, kc, vc, probs, d_outc, scale)
         inverse, offsets, counts = M.invert_routes(sel, nb)
         order = M.dkdv_tile_order(counts, B * H, S, D, be)
-        from vsa import _lib
+        from vsa_mi355x import _lib
         code, st = _lib.dtype_code(qd.dtype), _lib.stream_of(qd)
         dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
 
@@ -360,7 +360,7 @@ def main():
             "sparse_fwd": (_events_time(lambda: M.sparse_forward(qd, kd, vd, sel, vbs, be, scale,
                                                                  out_c=outc, gate=gd), it),
                            F_fwd),
-            "bwd_prep": (_events_time(lambda: M.backward_prep(out, do, be, out_c=outc, gate=gd),
+            "bwd_prep": (_events_time(lambda: M.backward_prep(fine, do, be, out_c=outc, gate=gd),
                                       it), None),
             "coarse_bwd": (_events_time(lambda: M.coarse_backward(qc, kc, vc, probs, d_outc,
                                                                   scale), it), None),

@@ -117,12 +117,15 @@ int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
  * (fused_common.py:175-199, 261-295):
  *   out = T(out_c[block] * gate + attn)   (gate = 1 when gate_mode == NONE)
  *   out = T(attn)                          when out_c == NULL
+ *   fine_out = T(attn)   when out_c != NULL and fine_out != NULL: the fine
+ *                        output the reference's fused path keeps as its own
+ *                        tensor (triton_impl.py:408); vsa_bwd_prep takes it
  *   lse[bh, q] = log2(sum_j exp2(scale*log2(e) * q.k_j))   (may be NULL)
  * block_elements in {64, 128, 256}; head_dim in {64, 128, 256}.
  */
 int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                    const int32_t* selected, const int32_t* kv_vbs,
-                   void* out, float* lse, const void* out_c, const void* gate,
+                   void* out, void* fine_out, float* lse, const void* out_c, const void* gate,
                    int32_t gate_mode, int32_t gate_heads, int64_t bh, int64_t sq, int64_t skv,
                    int32_t head_dim, int32_t block_elements, int32_t topk,
                    float scale, int32_t dtype, void* stream);
@@ -131,13 +134,14 @@ int vsa_sparse_fwd(const void* q, const void* k, const void* v,
  * Backward preprocessing over dout: the softmax delta plus the combine
  * gradients.  Replaces _delta_kernel/_delta_256_kernel (triton_impl.py:598-700)
  * and _FusedCombine.backward (fused_common.py:202-256, 298-337).
- *   attn  = out - out_c[block] * gate    (attn = out when out_c == NULL)
- *   delta[bh, q]   = sum_d attn * dout                               (fp32)
+ * fine_out is the fine output as stored in T: vsa_sparse_fwd's fine_out when
+ * the combine was fused (out_c != NULL), its out otherwise.
+ *   delta[bh, q]   = sum_d fine_out * dout                           (fp32)
  *   d_out_c[bh, n] = T(sum_{t < be} T(dout * gate))     (if out_c != NULL)
  *   d_gate         = T(dout * out_c[block])  (per token: summed over d),
  * d_gate in the gate's own layout (token-major included).
  */
-int vsa_bwd_prep(const void* out, const void* dout, const void* out_c, const void* gate,
+int vsa_bwd_prep(const void* fine_out, const void* dout, const void* out_c, const void* gate,
                  int32_t gate_mode, int32_t gate_heads, float* delta, void* d_out_c, void* d_gate,
                  int64_t bh, int64_t sq, int32_t head_dim, int32_t block_elements,
                  int32_t dtype, void* stream);

@@ -2,7 +2,7 @@
 
 This module is the checker, never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-import it.  The shipped path (``vsa.mi355x_vsa`` / ``vsa.mi355x_sparse_attention``)
+import it.  The shipped path (``vsa_mi355x.mi355x_vsa`` / ``vsa_mi355x.mi355x_sparse_attention``)
 runs the HIP kernels and fails loudly when they are missing.
 
 It restates, in plain PyTorch (fp32 math on the CPU unless the input dtype says

@@ -201,11 +201,14 @@ __global__ __launch_bounds__(256) void csr_sort_kernel(const int32_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// Backward preprocessing: one workgroup per (bh, query block).
+// Backward preprocessing: one workgroup per (bh, query block).  delta is the
+// row sum of the fine output as the forward stored it in T times dout (the
+// reference's delta over its stored sparse output, triton_impl.py:598-700),
+// never a difference recovered from the rounded combined output.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(
-    const T* __restrict__ out, const T* __restrict__ dout, const T* __restrict__ outc,
+    const T* __restrict__ fine, const T* __restrict__ dout, const T* __restrict__ outc,
     const T* __restrict__ gate, int gate_mode, int gate_heads, float* __restrict__ delta,
     T* __restrict__ d_outc, T* __restrict__ d_gate, int qb, int D, int be) {
   constexpr int VEC = 16 / sizeof(T);
@@ -234,7 +237,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const int64_t goff = gate_mode == 3
                              ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
                              : off;
-    u32x4 ro = *reinterpret_cast<const u32x4*>(out + off);
+    u32x4 ro = *reinterpret_cast<const u32x4*>(fine + off);
     u32x4 rd = *reinterpret_cast<const u32x4*>(dout + off);
     const T* o = reinterpret_cast<const T*>(&ro);
     const T* g = reinterpret_cast<const T*>(&rd);
@@ -254,8 +257,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float dov = Elem<T>::to_f(g[e]);
-      const float attn = outc ? Elem<T>::to_f(o[e]) - oc[e] * gv[e] : Elem<T>::to_f(o[e]);
-      dl = fmaf(attn, dov, dl);
+      dl = fmaf(Elem<T>::to_f(o[e]), dov, dl);
       dgv[e] = Elem<T>::from_f(dov * oc[e]);
       if (outc) {
         dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[e]);
@@ -452,11 +454,11 @@ extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* 
   return vsa_check_launch();
 }
 
-extern "C" int vsa_bwd_prep(const void* out, const void* dout, const void* out_c,
+extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* out_c,
                             const void* gate, int32_t gate_mode, int32_t gate_heads,
                             float* delta, void* d_out_c, void* d_gate, int64_t bh, int64_t sq,
                             int32_t D, int32_t be, int32_t dtype, void* stream) {
-  if (!out || !dout || !delta) return VSA_ERR_NULL;
+  if (!fine_out || !dout || !delta) return VSA_ERR_NULL;
   if (gate_mode < 0 || gate_mode > 3) return VSA_ERR_SHAPE;
   if (out_c && gate_mode == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
   if (out_c && !d_out_c) return VSA_ERR_NULL;
@@ -467,7 +469,7 @@ extern "C" int vsa_bwd_prep(const void* out, const void* dout, const void* out_c
   hipStream_t s = (hipStream_t)stream;
   VSA_DISPATCH_ALL(dtype, T, {
     hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3(qb, (unsigned)bh), dim3(256), 0, s,
-                       (const T*)out, (const T*)dout, (const T*)out_c, (const T*)gate, gate_mode,
+                       (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate, gate_mode,
                        gate_heads, delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
   });
   return vsa_check_launch();

@@ -9,7 +9,7 @@
 namespace vsa {
 
 int sparse_fwd_f32(const void* q, const void* k, const void* v, const int32_t* selected,
-                   const int32_t* kv_vbs, void* out, float* lse, const void* out_c,
+                   const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* out_c,
                    const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq,
                    int64_t skv, int D, int be, int topk, float scale, hipStream_t s);
 

@@ -157,9 +157,10 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(F32Cfg<D>::
 sparse_fwd_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k,
                        const float* __restrict__ v, const int32_t* __restrict__ selected,
                        const int32_t* __restrict__ kv_vbs, float* __restrict__ out,
-                       float* __restrict__ lse, const float* __restrict__ outc,
-                       const float* __restrict__ gate, int gate_mode, int gate_heads,
-                       int tiles_per_head, int sq, int skv, int qb, int kb, int topk, float c2) {
+                       float* __restrict__ fine, float* __restrict__ lse,
+                       const float* __restrict__ outc, const float* __restrict__ gate,
+                       int gate_mode, int gate_heads, int tiles_per_head, int sq, int skv, int qb,
+                       int kb, int topk, float c2) {
   using C = F32Cfg<D>;
   constexpr int LD = C::LD;
   __shared__ __attribute__((aligned(16))) float ks[kChunk * LD];
@@ -233,6 +234,7 @@ sparse_fwd_f32m_kernel(const float* __restrict__ q, const float* __restrict__ k,
       f32x4 val;
 #pragma unroll
       for (int e = 0; e < 4; ++e) val[e] = o[mt][4 * g + e] * inv;
+      if (ocrow && fine) *reinterpret_cast<f32x4*>(fine + tok * D + d0) = val;
       if (ocrow) {
         const f32x4 oc = *reinterpret_cast<const f32x4*>(ocrow + d0);
         const f32x4 gv = grow ? *reinterpret_cast<const f32x4*>(grow + d0)
@@ -570,7 +572,7 @@ static bool f32_shape(int D, int be) {
   X(64, 64) X(64, 128) X(64, 256) X(128, 64) X(128, 128) X(128, 256) X(256, 64) X(256, 128) X(256, 256)
 
 int sparse_fwd_f32(const void* q, const void* k, const void* v, const int32_t* selected,
-                   const int32_t* kv_vbs, void* out, float* lse, const void* out_c,
+                   const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* out_c,
                    const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq,
                    int64_t skv, int D, int be, int topk, float scale, hipStream_t s) {
   if (!f32_shape(D, be)) return VSA_ERR_UNSUPPORTED;
@@ -582,9 +584,9 @@ int sparse_fwd_f32(const void* q, const void* k, const void* v, const int32_t* s
   if (D == DD && be == BB) {                                                                 \
     hipLaunchKernelGGL((sparse_fwd_f32m_kernel<DD, BB>), dim3((unsigned)tiles), dim3(128), 0, \
                        s, (const float*)q, (const float*)k, (const float*)v, selected, kv_vbs, \
-                       (float*)out, lse, (const float*)out_c, (const float*)gate, gate_mode,  \
-                       gate_heads, tph, (int)sq, (int)skv, (int)(sq / BB), (int)(skv / BB),  \
-                       topk, c2);                                                            \
+                       (float*)out, (float*)fine, lse, (const float*)out_c,                \
+                       (const float*)gate, gate_mode, gate_heads, tph, (int)sq, (int)skv,     \
+                       (int)(sq / BB), (int)(skv / BB), topk, c2);                           \
     return vsa_check_launch();                                                               \
   }
   VSA_F32_SHAPES(VSA_F)

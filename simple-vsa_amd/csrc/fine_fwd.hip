@@ -50,7 +50,7 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units
 template <typename T, int D>
 __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float lsum, float m,
                                              int64_t b, int myq, int qblk, int h, int sq, int qb,
-                                             T* __restrict__ out, float* __restrict__ lse,
+                                             T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse,
                                              const T* __restrict__ outc,
                                              const T* __restrict__ gate, int gate_mode,
                                              int gate_heads) {
@@ -107,6 +107,19 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
       *reinterpret_cast<u32x2*>(out + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
     }
   }
+  if (ocrow && fine) {  // the fine output as stored in T, for the backward's delta
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        T f4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f4[e] = E::from_f(oacc[mt][4 * g + e] * inv);
+        *reinterpret_cast<u32x2*>(fine + tok * D + mt * 32 + 8 * g + 4 * h) =
+            *reinterpret_cast<const u32x2*>(f4);
+      }
+    }
+  }
   // stored last: a load issued after a store also waits for that store
   if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
 }
@@ -115,7 +128,7 @@ template <typename T, int D, int BE>
 __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(FwdCfg<D, BE>::WPE))) void sparse_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
-    T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
+    T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
     const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles, int tiles_per_head, int sq,
     int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
   using C = FwdCfg<D, BE>;
@@ -252,7 +265,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
   }
 
-  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, lse, outc, gate, gate_mode,
+  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate, gate_mode,
                      gate_heads);
 }
 
@@ -285,7 +298,7 @@ template <typename T, int D>
 __device__ __forceinline__ void fwd_pp_tile(
     T* smem, int tile, const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
-    T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
+    T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
     const T* __restrict__ gate, int gate_mode, int gate_heads, int sq, int skv, int qb, int kb,
     int topk, float c2, uint32_t qsign) {
   constexpr int BE = 256;
@@ -565,7 +578,7 @@ __device__ __forceinline__ void fwd_pp_tile(
     }
   }
   if (!grp1) phase_barrier();
-  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, lse, outc, gate, gate_mode,
+  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate, gate_mode,
                      gate_heads);
 }
 
@@ -577,7 +590,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
                      const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
-                     T* __restrict__ out, float* __restrict__ lse, const T* __restrict__ outc,
+                     T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
                      const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles,
                      int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
   using C = FwdPPCfg<D>;
@@ -586,7 +599,7 @@ sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
   for (int j = (int)(blockIdx.x >> 3); j < per; j += stride) {
     const int tile = xcd * per + j;
     if (tile >= num_tiles) break;
-    fwd_pp_tile<T, D>(smem, tile, q, k, v, selected, kv_vbs, out, lse, outc, gate, gate_mode,
+    fwd_pp_tile<T, D>(smem, tile, q, k, v, selected, kv_vbs, out, fine, lse, outc, gate, gate_mode,
                       gate_heads, sq, skv, qb, kb, topk, c2, qsign);
     dma_wait();
     __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
@@ -595,7 +608,7 @@ sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
 
 template <typename T, int D>
 static int launch_fwd_pp(const void* q, const void* k, const void* v, const int32_t* selected,
-                         const int32_t* kv_vbs, void* out, float* lse, const void* outc,
+                         const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* outc,
                          const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq,
                          int64_t skv, int topk, float scale, hipStream_t stream) {
   const int64_t tiles = bh * (sq / 256);
@@ -606,7 +619,7 @@ static int launch_fwd_pp(const void* q, const void* k, const void* v, const int3
   const float c2 = fabsf(scale) * kLog2e;
   const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
   hipLaunchKernelGGL((sparse_fwd_pp_kernel<T, D>), dim3(grid), dim3(512), 0, stream,
-                     (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, lse,
+                     (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, (T*)fine, lse,
                      (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, (int)sq,
                      (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign);
   return vsa_check_launch();
@@ -614,7 +627,7 @@ static int launch_fwd_pp(const void* q, const void* k, const void* v, const int3
 
 template <typename T, int D, int BE>
 static int launch_fwd(const void* q, const void* k, const void* v, const int32_t* selected,
-                      const int32_t* kv_vbs, void* out, float* lse, const void* outc,
+                      const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* outc,
                       const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq, int64_t skv,
                       int topk, float scale, hipStream_t stream) {
   using C = FwdCfg<D, BE>;
@@ -625,7 +638,7 @@ static int launch_fwd(const void* q, const void* k, const void* v, const int32_t
   const float c2 = fabsf(scale) * kLog2e;
   const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
   hipLaunchKernelGGL((sparse_fwd_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
-                     (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, lse,
+                     (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, (T*)fine, lse,
                      (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, tph, (int)sq,
                      (int)skv, (int)(sq / BE), (int)(skv / BE), topk, c2, qsign);
   return vsa_check_launch();
@@ -640,7 +653,7 @@ using namespace vsa;
 // give every CU one (smaller grids run better as 4-wave half-block workgroups)
 #define VSA_FWD_PP_CASE(DD)                                                                    \
   if (D == DD && be == 256 && bh * (sq / 256) >= 256)                                          \
-    return launch_fwd_pp<T, DD>(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode,   \
+    return launch_fwd_pp<T, DD>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c, gate, gate_mode,   \
                                 gate_heads, bh, sq, skv, topk, scale, s);
 #else
 #define VSA_FWD_PP_CASE(DD)
@@ -648,25 +661,28 @@ using namespace vsa;
 
 #define VSA_FWD_CASE(DD, BB)                                                                   \
   if (D == DD && be == BB)                                                                     \
-    return launch_fwd<T, DD, BB>(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode, gate_heads, \
+    return launch_fwd<T, DD, BB>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c, gate, gate_mode, gate_heads, \
                                  bh, sq, skv, topk, scale, s);
 
 extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                               const int32_t* selected, const int32_t* kv_vbs, void* out,
-                              float* lse, const void* out_c, const void* gate, int32_t gate_mode,
+                              void* fine_out, float* lse, const void* out_c, const void* gate, int32_t gate_mode,
                               int32_t gate_heads, int64_t bh, int64_t sq, int64_t skv, int32_t D,
                               int32_t be, int32_t topk, float scale, int32_t dtype, void* stream) {
   if (!q || !k || !v || !selected || !kv_vbs || !out) return VSA_ERR_NULL;
   if (gate_mode < 0 || gate_mode > 3) return VSA_ERR_SHAPE;
   if (out_c && gate_mode == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
   if (out_c && gate_mode != 0 && !gate) return VSA_ERR_NULL;
-  if (!out_c) gate_mode = 0;
+  if (!out_c) {  // without the combine, out is the fine output
+    gate_mode = 0;
+    fine_out = nullptr;
+  }
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == VSA_F32)
-    return sparse_fwd_f32(q, k, v, selected, kv_vbs, out, lse, out_c, gate, gate_mode,
+    return sparse_fwd_f32(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c, gate, gate_mode,
                           gate_heads, bh, sq, skv, D, be, topk, scale, s);
   VSA_DISPATCH_MFMA(dtype, T, {
     VSA_FWD_PP_CASE(128)

@@ -1,9 +1,14 @@
-"""MI355X-native Video Sparse Attention.
+"""MI355X-native Video Sparse Attention (package ``vsa_mi355x``).
 
-Importing ``vsa`` needs only torch; the gfx950 kernel library is loaded on the
-first call, as the reference loads its GPU backends (vsa/__init__.py:28-69).
-The tiling helpers and the gate producer keep the reference's names
-(vsa/__init__.py:7, 10-25).
+The package is named apart from the reference's own ``vsa`` package so that
+both can be imported in one process: the reference registers this backend in
+its ``vsa`` namespace with a lazy loader (vsa/__init__.py:28-69 is how it
+registers ``triton_vsa`` and the others), and the loader imports
+``vsa_mi355x.mi355x`` on the first call.
+
+Importing ``vsa_mi355x`` needs only torch; the gfx950 kernel library is loaded
+on the first call.  The tiling helpers and the gate producer keep the
+reference's names (vsa/__init__.py:7, 10-25).
 """
 
 from typing import Any
@@ -16,21 +21,21 @@ __all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_sparse_executor", "m
 
 
 def mi355x_vsa(*args: Any, **kwargs: Any) -> Any:
-    """Full VSA (coarse + routed fine branch) on MI355X; see ``vsa.mi355x``."""
+    """Full VSA (coarse + routed fine branch) on MI355X; see ``vsa_mi355x.mi355x``."""
     from .mi355x import mi355x_vsa as _impl
 
     return _impl(*args, **kwargs)
 
 
 def mi355x_sparse_attention(*args: Any, **kwargs: Any) -> Any:
-    """Route-explicit sparse executor on MI355X; see ``vsa.mi355x``."""
+    """Route-explicit sparse executor on MI355X; see ``vsa_mi355x.mi355x``."""
     from .mi355x import mi355x_sparse_attention as _impl
 
     return _impl(*args, **kwargs)
 
 
 def mi355x_sparse_executor(*args: Any, **kwargs: Any) -> Any:
-    """Sparse-executor callable for a shared orchestrator; see ``vsa.mi355x``."""
+    """Sparse-executor callable for a shared orchestrator; see ``vsa_mi355x.mi355x``."""
     from .mi355x import mi355x_sparse_executor as _impl
 
     return _impl(*args, **kwargs)

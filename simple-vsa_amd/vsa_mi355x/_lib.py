@@ -33,8 +33,8 @@ SIGNATURES = {
     "vsa_coarse_fwd": [_P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _F, _I32, _P],
     "vsa_topk": [_P, _P, _I64, _I32, _I32, _P],
     "vsa_csr_build": [_P, _P, _P, _P, _I64, _I32, _I32, _I32, _P],
-    "vsa_sparse_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I64, _I64, _I64, _I32,
-                       _I32, _I32, _F, _I32, _P],
+    "vsa_sparse_fwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I64, _I64, _I64,
+                       _I32, _I32, _I32, _F, _I32, _P],
     "vsa_bwd_prep": [_P, _P, _P, _P, _I32, _I32, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P],
     "vsa_coarse_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _F, _I32, _P],
     "vsa_sparse_bwd_dq": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I32,

@@ -258,17 +258,24 @@ def invert_routes(selected: Tensor, key_blocks: int):
 
 def sparse_forward(q, k, v, selected, variable_block_sizes, block_elements, scale, *,
                    out_c=None, gate=None, want_lse=True):
-    """Fine forward (+ combine when ``out_c`` is given).  Returns (out, lse)."""
+    """Fine forward (+ combine when ``out_c`` is given).  Returns (out, lse, fine):
+    with the combine and ``want_lse``, ``fine`` is the fine output as stored in
+    T, which the backward's delta needs (triton_impl.py:408, 598-700); else
+    ``fine`` is ``out`` (no combine) or None (no backward)."""
     b, h, sq, d = q.shape
     skv = k.shape[2]
     out = torch.empty_like(q)
     lse = (torch.empty((b, h, sq), device=q.device, dtype=torch.float32) if want_lse else None)
+    fine = torch.empty_like(q) if (want_lse and out_c is not None) else None
     gmode = _gate_mode(gate, d) if out_c is not None else _lib.GATE_NONE
     _lib.call("vsa_sparse_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(selected),
-              _lib.ptr(variable_block_sizes), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(out_c),
-              _lib.ptr(gate if gmode else None), gmode, h, b * h, sq, skv, d, block_elements,
-              selected.shape[-1], float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
-    return out, lse
+              _lib.ptr(variable_block_sizes), _lib.ptr(out), _lib.ptr(fine), _lib.ptr(lse),
+              _lib.ptr(out_c), _lib.ptr(gate if gmode else None), gmode, h, b * h, sq, skv, d,
+              block_elements, selected.shape[-1], float(scale), _lib.dtype_code(q.dtype),
+              _lib.stream_of(q))
+    if out_c is None and want_lse:
+        fine = out
+    return out, lse, fine
 
 
 def _token_major(gate: Tensor) -> bool:
@@ -286,8 +293,10 @@ def _gate_mode(gate: Optional[Tensor], d: int) -> int:
     return _lib.GATE_TOKEN_MAJOR if _token_major(gate) else _lib.GATE_FULL
 
 
-def backward_prep(out, dout, block_elements, *, out_c=None, gate=None):
-    """delta (fp32) and, with the combine, (d_out_c, d_gate)."""
+def backward_prep(fine, dout, block_elements, *, out_c=None, gate=None):
+    """delta (fp32, from the fine output ``fine`` as stored in T) and, with the
+    combine, (d_out_c, d_gate)."""
+    out = fine
     b, h, sq, d = out.shape
     delta = torch.empty((b, h, sq), device=out.device, dtype=torch.float32)
     d_outc = torch.empty_like(out_c) if out_c is not None else None
@@ -359,7 +368,8 @@ def dkdv_tile_order(counts, bh, skv, head_dim, block_elements):
 class _SparseAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, selected, vbs, block_elements, scale):
-        out, lse = sparse_forward(q, k, v, selected, vbs, block_elements, scale, want_lse=True)
+        out, lse, _ = sparse_forward(q, k, v, selected, vbs, block_elements, scale,
+                                     want_lse=True)
         ctx.save_for_backward(q, k, v, out, lse, selected, vbs)
         ctx.block_elements, ctx.scale = block_elements, scale
         return out
@@ -440,17 +450,17 @@ class _VSA(torch.autograd.Function):
     def forward(ctx, q, k, v, gate, vbs, qvbs, topk_, be, scale):
         qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
         _, probs, outc, sel = coarse_forward(qc, kc, vc, topk_, scale)
-        out, lse = sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
-                                  want_lse=True)
-        ctx.save_for_backward(q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, out, lse)
+        out, lse, fine = sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
+                                        want_lse=True)
+        ctx.save_for_backward(q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, fine, lse)
         ctx.be, ctx.scale = be, scale
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, out, lse = ctx.saved_tensors
+        q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, fine, lse = ctx.saved_tensors
         dout = dout.contiguous()
-        delta, d_outc, d_gate = backward_prep(out, dout, ctx.be, out_c=outc, gate=gate)
+        delta, d_outc, d_gate = backward_prep(fine, dout, ctx.be, out_c=outc, gate=gate)
         dqc, dkc, dvc = coarse_backward(qc, kc, vc, probs, d_outc, ctx.scale)
         dq, dk, dv = sparse_backward(q, k, v, dout, lse, delta, sel, vbs, ctx.be, ctx.scale,
                                      dqc=dqc, dkc=dkc, dvc=dvc, q_variable_block_sizes=qvbs)

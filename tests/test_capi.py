@@ -9,8 +9,8 @@ import re
 import pytest
 import torch
 
-from vsa import _lib
-from vsa import mi355x as M
+from vsa_mi355x import _lib
+from vsa_mi355x import mi355x as M
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "vsa_capi.h")
@@ -58,16 +58,16 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.vsa_dkdv_tile_order(p, p, 23, 1, 1024, 128, 256, None) == -2   # 8 tiles
     assert lib.vsa_dkdv_tile_order(p, p, 64, 1, 1024, 128, 96, None) == -2   # 1024 % 96
     assert lib.vsa_dkdv_tile_order(p, p, 64, 1, 960, 128, 96, None) == -4    # no kernel
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, None, 0, 0,
                               1, 100, 128, 128, 64, 1, 0.1, 0, None) == -2   # 100 % 64
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, None, 0, 0,
                               1, 96, 96, 128, 96, 1, 0.1, 0, None) == -4     # be 96: no kernel
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, None, 0, 0,
                               1, 64, 64, 128, 64, 1, 0.1, 7, None) == -3     # no dtype 7
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, 0, 0,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, None, None, 0, 0,
                               1, 96, 96, 128, 96, 1, 0.1, 2, None) == -4     # fp32, be 96
     # token-major gate: the heads count must divide batch*heads
-    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, p, p, 3, 3,
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, p, p, 3, 3,
                               4, 64, 64, 128, 64, 1, 0.1, 0, None) == -2
     assert lib.vsa_bwd_prep(p, p, p, p, 3, 0, p, p, p, 4, 64, 128, 64, 0, None) == -2
     # tiling entry points validate before launching

@@ -4,8 +4,8 @@
 import pytest
 import torch
 
-from vsa import CompressionGate
-from vsa import mi355x as M
+from vsa_mi355x import CompressionGate
+from vsa_mi355x import mi355x as M
 
 
 def test_compression_gate_shape_and_layout():

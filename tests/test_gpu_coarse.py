@@ -20,7 +20,7 @@ DEV = "cuda"
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
@@ -52,7 +52,7 @@ SIZES = [(1, 1), (45, 37), (33, 70), (7, 258), (320, 320), (640, 640)]
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("qb,kb", SIZES)
 def test_coarse_forward_mfma_matches_oracle(dtype, D, qb, kb):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(qb * 1000 + kb + D)
     bh, tk = 3, min(8, kb)
     qc, kc, vc = (torch.randn(1, bh, n, D, generator=g).to(dtype) for n in (qb, kb, kb))
@@ -82,7 +82,7 @@ def test_coarse_forward_mfma_matches_oracle(dtype, D, qb, kb):
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("qb,kb", [(1, 1), (45, 37), (33, 70), (320, 320), (640, 640)])
 def test_coarse_backward_mfma_matches_oracle_autograd(dtype, D, qb, kb):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(qb * 7 + kb + D)
     bh = 2
     qc, kc, vc = (torch.randn(1, bh, n, D, generator=g).to(dtype) for n in (qb, kb, kb))
@@ -102,7 +102,7 @@ def test_coarse_backward_mfma_matches_oracle_autograd(dtype, D, qb, kb):
 
 
 def test_coarse_backward_is_deterministic():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(3)
     qc, kc, vc, do = (torch.randn(1, 4, 200, 128, generator=g).to(torch.bfloat16).to(DEV)
                       for _ in range(4))
@@ -120,7 +120,7 @@ def test_coarse_backward_is_deterministic():
 @pytest.mark.parametrize("kb,tk", [(1, 1), (5, 5), (300, 1), (300, 300), (4096, 64),
                                    (4096, 4095), (1000, 999)])
 def test_topk_radix_sizes_with_ties(kb, tk):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     rng = np.random.default_rng(kb + tk)
     scores = torch.from_numpy(rng.integers(-3, 4, size=(5, kb)).astype(np.float32) / 4)
     got = M.topk(scores.to(DEV), tk).cpu().numpy()
@@ -128,7 +128,7 @@ def test_topk_radix_sizes_with_ties(kb, tk):
 
 
 def test_topk_radix_special_values():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     inf = float("inf")
     rows = torch.tensor([
         [0.0, -0.0, 0.0, -0.0, 1e-30, -1e-30],      # -0 == +0: ties go to smaller ids
@@ -150,7 +150,7 @@ def test_topk_radix_special_values():
 
 def test_topk_radix_one_distinct_winner_many_ties_below():
     # the k-th value is shared by most of the row: the last digit pass resolves it
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     kb = 2048
     row = torch.full((2, kb), 0.5)
     row[0, 1000] = 0.75

@@ -28,7 +28,7 @@ DEV = "cuda"
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
@@ -57,7 +57,7 @@ def _inputs(B, H, S, D, seed, amp=1.0, gate=None, dtype=torch.bfloat16):
 
 
 def _run_full(q, k, v, do, gate, vbs, topk, block):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     leaves = [t.detach().clone().requires_grad_() for t in (q, k, v)]
     gl = gate.detach().clone().requires_grad_() if gate is not None else None
     out = M.mi355x_vsa(*leaves, vbs, vbs, topk, block, gl)
@@ -81,7 +81,7 @@ def _oracle_heads(q, k, v, do, gate, vbs, topk, block, sel, heads):
 
 def _full_config_case(B, H, S, D, block, topk, vbs_list, gate_kind, seed, heads, amp=1.0,
                       dtype=torch.bfloat16):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     be = math.prod(block)
     vbs = torch.tensor(vbs_list, device=DEV, dtype=torch.int32)
     q, k, v, do, gate = _inputs(B, H, S, D, seed, amp, gate_kind, dtype)
@@ -145,7 +145,7 @@ def _zipf_routes(h, qb, kb, tk, seed):
 def test_c5_route_skew_explicit_routing():
     # H=24, S=40960, D=64, block 64 (640 blocks), topk 32, Zipf(1.2)
     # routes drawn without replacement; explicit-route entry point
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     B, H, S, D, be, tk = 1, 24, 40960, 64, 64, 32
     nb = S // be
     sel = _zipf_routes(H, nb, nb, tk, 5)

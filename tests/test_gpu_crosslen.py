@@ -18,7 +18,7 @@ DEV = "cuda"
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
@@ -46,7 +46,7 @@ CASES = [((4, 8, 8), 128, 3, 7, 2, torch.bfloat16, "full"),
 
 @pytest.mark.parametrize("block,D,nq,nk,topk,dtype,gate_kind", CASES)
 def test_full_op_with_different_query_and_key_lengths(block, D, nq, nk, topk, dtype, gate_kind):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     be = math.prod(block)
     B, H = 1, 2
     print(f"cross-length block={block} D={D} Sq={nq * be} Skv={nk * be} {dtype}", flush=True)
@@ -85,7 +85,7 @@ def test_full_op_with_different_query_and_key_lengths(block, D, nq, nk, topk, dt
                                            (2, 2, 128, 256, 3, 4), (1, 64, 256, 128, 4, 6),
                                            (1, 32, 256, 64, 8, 3)])
 def test_explicit_route_with_different_query_and_key_lengths(B, H, be, D, nq, nk):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     topk = 3
     g = torch.Generator().manual_seed(be + nq + nk)
     q = torch.randn(B, H, nq * be, D, generator=g).to(torch.bfloat16)

@@ -30,7 +30,7 @@ CASES = [((1, 1, 64), 64, 12, 3, None), ((1, 1, 64), 128, 9, 4, "full"),
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
@@ -57,7 +57,7 @@ def _gate(kind, B, H, S, D, g):
 
 @pytest.mark.parametrize("block,D,nb,topk,gate_kind", CASES)
 def test_fp32_vsa_matches_oracle(block, D, nb, topk, gate_kind):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     be = math.prod(block)
     B, H, S = 1, 2, be * nb
     print(f"fp32 vsa block={block} D={D} nb={nb} topk={topk} gate={gate_kind}", flush=True)
@@ -95,7 +95,7 @@ def test_fp32_vsa_matches_oracle(block, D, nb, topk, gate_kind):
 @pytest.mark.parametrize("be,D,scale", [(64, 64, None), (256, 128, -0.05), (128, 256, 0.2),
                                         (16, 96, None)])
 def test_fp32_explicit_route_matches_oracle(be, D, scale):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     B, H, nb, topk = 2, 2, 9, 4
     S = be * nb
     print(f"fp32 explicit route be={be} D={D} scale={scale}", flush=True)
@@ -122,7 +122,7 @@ def test_fp32_explicit_route_matches_oracle(be, D, scale):
 def test_fp32_lse_matches_oracle():
     """The saved base-2 log-sum-exp of the fp32 forward (used by both backward
     kernels) against the oracle's m + log2(l)."""
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     be, D, nb, topk = 128, 128, 6, 3
     S = be * nb
     g = torch.Generator(device=DEV).manual_seed(7)
@@ -132,7 +132,7 @@ def test_fp32_lse_matches_oracle():
     vbs = torch.full((nb,), be, dtype=torch.int32)
     vbs[0] = 77
     scale = 1.0 / math.sqrt(D)
-    out, lse = M.sparse_forward(q, k, v, sel.to(DEV), vbs.to(DEV), be, scale, want_lse=True)
+    out, lse, _ = M.sparse_forward(q, k, v, sel.to(DEV), vbs.to(DEV), be, scale, want_lse=True)
     ref_out, ref_lse = O.sparse_attention_reference(q.cpu(), k.cpu(), v.cpu(), sel, vbs, be, scale)
     _check(out, ref_out, "out")
     _check(lse, ref_lse, "lse")

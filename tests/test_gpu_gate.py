@@ -16,13 +16,13 @@ DEV = "cuda"
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
 
 def _grads(q, k, v, gate, vbs, topk, block, do):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     leaves = [t.detach().clone().requires_grad_() for t in (q, k, v)]
     g = gate.detach().clone() if gate.is_contiguous() else \
         gate.detach().transpose(1, 2).clone().transpose(1, 2)
@@ -40,7 +40,7 @@ def test_token_major_gate_is_bit_identical_to_contiguous_gate(B, H, S, D, be, to
                    for _ in range(4))
     # the producer's layout: [B, S, H, D] contiguous, viewed per head
     g_tm = torch.rand(B, S, H, D, generator=gen, device=DEV, dtype=torch.bfloat16).transpose(1, 2)
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     assert M._token_major(g_tm)
     vbs = torch.full((S // be,), be, device=DEV, dtype=torch.int32)
     vbs[-1] = be - 7
@@ -54,8 +54,8 @@ def test_token_major_gate_is_bit_identical_to_contiguous_gate(B, H, S, D, be, to
 
 
 def test_gate_producer_trains_end_to_end_against_oracle():
-    from vsa import CompressionGate
-    from vsa import mi355x as M
+    from vsa_mi355x import CompressionGate
+    from vsa_mi355x import mi355x as M
     torch.manual_seed(1)
     B, H, D, be, nb = 1, 2, 64, 64, 6
     S, dim = be * nb, H * D

@@ -19,7 +19,7 @@ DEV = "cuda"
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
@@ -27,7 +27,7 @@ def _gpu_only():
 @pytest.mark.parametrize("be,D,nb,dtype", [(256, 128, 3, torch.bfloat16), (64, 64, 5, torch.bfloat16),
                                           (128, 256, 2, torch.bfloat16), (64, 128, 4, torch.float32)])
 def test_all_blocks_selected_is_dense_attention(be, D, nb, dtype):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(be + D)
     B, H, S = 1, 2, nb * be
     q, k, v, do = (torch.randn(B, H, S, D, generator=g).to(dtype) for _ in range(4))
@@ -48,7 +48,7 @@ def test_all_blocks_selected_is_dense_attention(be, D, nb, dtype):
 
 
 def test_gate_zero_and_two():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator(device=DEV).manual_seed(3)
     be, D, nb, topk = 256, 128, 4, 2
     q, k, v = (torch.randn(1, 2, nb * be, D, generator=g, device=DEV, dtype=torch.bfloat16)
@@ -69,7 +69,7 @@ def test_gate_zero_and_two():
 
 
 def test_unrouted_key_blocks_still_get_gradient():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator(device=DEV).manual_seed(5)
     be, D, nb, topk = 64, 64, 8, 1
     q, k, v = (torch.randn(1, 1, nb * be, D, generator=g, device=DEV, dtype=torch.bfloat16)

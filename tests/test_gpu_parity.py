@@ -29,7 +29,7 @@ def _need_gpu():
 @pytest.fixture(autouse=True)
 def _gpu_only():
     _need_gpu()
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()          # fail loudly (not skip) when the kernels are not built
     yield
 
@@ -59,7 +59,7 @@ def _gpu(*ts):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("be,vbs", [(64, [64, 37, 11]), (256, [256, 191, 73, 0])])
 def test_block_mean_matches_oracle(dtype, be, vbs):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(11)
     nb = len(vbs)
     q = _randn((1, 2, nb * be, 128), g, dtype)
@@ -85,7 +85,7 @@ def test_block_mean_matches_oracle(dtype, be, vbs):
 
 @pytest.mark.parametrize("kb,tk", [(13, 5), (160, 20), (360, 45), (640, 32)])
 def test_topk_bit_exact_with_ties(kb, tk):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     rng = np.random.default_rng(kb)
     # coarse values produce many exact ties at the k-th boundary
     scores = torch.from_numpy(rng.integers(-6, 7, size=(3, 37, kb)).astype(np.float32) / 8)
@@ -95,7 +95,7 @@ def test_topk_bit_exact_with_ties(kb, tk):
 
 
 def test_topk_agrees_with_torch_topk_on_untied_rows():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(5)
     scores = torch.randn(2, 4, 50, 160, generator=g)
     got = M.topk(scores.to(DEV), 20).cpu()
@@ -109,7 +109,7 @@ def test_topk_agrees_with_torch_topk_on_untied_rows():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_coarse_forward_matches_oracle_and_routes_by_its_own_scores(dtype):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(7)
     b, h, be, nb, d = 1, 3, 64, 40, 128
     q, k, v = (_randn((b, h, nb * be, d), g, dtype) for _ in range(3))
@@ -152,7 +152,7 @@ def _zipf_routes(h, qb, kb, tk, seed):
 
 @pytest.mark.parametrize("case", ["random", "zipf", "hot", "duplicates"])
 def test_csr_bit_exact(case):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     if case == "random":
         kb = 13
         sel = torch.randn(2, 3, 7, kb, generator=torch.Generator().manual_seed(17)).topk(
@@ -175,7 +175,7 @@ def test_csr_bit_exact(case):
 
 
 def test_csr_ignores_out_of_range_ids():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     sel = torch.tensor([[[[0, 5], [-1, 1], [2, 9]]]], dtype=torch.int32)
     inv, off, cnt = M.invert_routes(sel.to(DEV), 3)
     assert cnt.cpu().tolist() == [[[1, 1, 1]]]
@@ -200,7 +200,7 @@ def _route(h, qb, kb, tk, seed):
     (128, 64, [128, 100, 128], 2),
 ])
 def test_sparse_attention_fwd_bwd_matches_oracle(dtype, be, d, vbs, tk):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(31)
     h, nb = 2, len(vbs)
     q, k, v, do = (_randn((1, h, nb * be, d), g, dtype) for _ in range(4))
@@ -220,13 +220,13 @@ def test_sparse_attention_fwd_bwd_matches_oracle(dtype, be, d, vbs, tk):
 
 
 def test_sparse_forward_lse_matches_oracle():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(41)
     be, d, h = 256, 128, 2
     vbs = torch.tensor([256, 200, 256, 7])
     q, k, v = (_randn((1, h, 4 * be, d), g, torch.bfloat16) for _ in range(3))
     sel = _route(h, 4, 4, 3, 9)
-    out, lse = M.sparse_forward(*_gpu(q, k, v, sel, vbs.to(torch.int32)), be, d ** -0.5)
+    out, lse, _ = M.sparse_forward(*_gpu(q, k, v, sel, vbs.to(torch.int32)), be, d ** -0.5)
     ref_out, ref_lse = O.sparse_attention_reference(q, k, v, sel, vbs, be, d ** -0.5)
     assert_parity(out, ref_out, what="out")
     torch.testing.assert_close(lse.cpu(), ref_lse.float(), atol=2e-3, rtol=1e-4)
@@ -234,7 +234,7 @@ def test_sparse_forward_lse_matches_oracle():
 
 def test_hot_kv_every_query_block_routes_to_block_zero():
     # tests/test_helion_vsa.py:332-403: KV ownership under maximal in-degree
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(51)
     be, nb, h, d = 256, 3, 2, 128
     q, k, v, do = (_randn((1, h, be * nb, d), g, torch.bfloat16) for _ in range(4))
@@ -255,7 +255,7 @@ def test_hot_kv_every_query_block_routes_to_block_zero():
 
 
 def test_negative_and_custom_scale():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(43)
     be, d, h = 64, 64, 1
     vbs = torch.tensor([64, 50, 64])
@@ -274,7 +274,7 @@ def test_sparse_executor_protocol():
     then execute(q, k, v, selected, vbs, sm_scale=scale) for the fine branch;
     the fine branch equals mi355x_sparse_attention on the same route, bitwise,
     in value and gradient, and matches the oracle."""
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(44)
     be, d, h, nb, tk = 256, 128, 2, 5, 2
     vbs = torch.tensor([256, 256, 200, 256, 256])
@@ -302,7 +302,7 @@ def test_sparse_executor_protocol():
 # ---------------------------------------------------------------------------
 
 def _full_vsa_case(dtype, be, d, h, vbs, tk, gate_kind, seed):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(seed)
     nb = len(vbs)
     shape = (1, h, nb * be, d)
@@ -363,7 +363,7 @@ def test_full_vsa_be64_d64_many_blocks():
 
 
 def test_full_vsa_route_matches_oracle_topk_on_identical_scores():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(45)
     be, nb, d, h, tk = 64, 24, 128, 3, 5
     q, k, v = (_randn((1, h, nb * be, d), g, torch.bfloat16) for _ in range(3))
@@ -382,7 +382,7 @@ def test_full_vsa_route_matches_oracle_topk_on_identical_scores():
 
 
 def test_full_vsa_is_deterministic():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(47)
     be, nb, d, h = 256, 6, 128, 2
     q, k, v, do = (_randn((1, h, nb * be, d), g, torch.bfloat16) for _ in range(4))
@@ -398,7 +398,7 @@ def test_full_vsa_is_deterministic():
 
 
 def test_no_grad_forward_equals_grad_forward():
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(49)
     be, nb, d, h = 64, 5, 128, 2
     q, k, v = (_randn((1, h, nb * be, d), g, torch.bfloat16).to(DEV) for _ in range(3))
@@ -408,3 +408,40 @@ def test_no_grad_forward_equals_grad_forward():
         a = M.mi355x_vsa(q, k, v, vbs, vbs, 2, (1, 1, be), gate)
     b = M.mi355x_vsa(q.requires_grad_(), k, v, vbs, vbs, 2, (1, 1, be), gate)
     assert torch.equal(a, b.detach())
+
+
+def test_registry_loader_full_op_parity(tmp_path, monkeypatch):
+    """The full op called the way the reference's users call a backend: through
+    a lazy loader in a ``vsa`` package (vsa/__init__.py:28-33), here a stand-in
+    written with the loaders the integration notes give."""
+    import importlib
+    import sys
+    from test_registry import _stub_package
+    monkeypatch.syspath_prepend(str(_stub_package(tmp_path)))
+    for name in [m for m in sys.modules if m == "vsa" or m.startswith("vsa.")]:
+        monkeypatch.delitem(sys.modules, name)
+    vsa = importlib.import_module("vsa")
+    from vsa_mi355x import mi355x as M
+    g = torch.Generator().manual_seed(65)
+    be, nb, h, d, tk = 256, 6, 2, 128, 3
+    shape = (1, h, nb * be, d)
+    q, k, v, do = (_randn(shape, g, torch.bfloat16) for _ in range(4))
+    gate = torch.rand(shape, generator=g).to(torch.bfloat16)
+    vbs = torch.tensor([256, 256, 190, 256, 256, 256])
+    qg, kg, vg, gg = (x.to(DEV).requires_grad_() for x in (q, k, v, gate))
+    out = vsa.mi355x_vsa(qg, kg, vg, vbs.to(DEV), vbs.to(DEV), tk, (4, 8, 8),
+                         compress_attn_weight=gg)
+    out.backward(do.to(DEV))
+    _, sel = M.mi355x_route(qg.detach(), kg.detach(), vg.detach(), vbs.to(DEV), vbs.to(DEV), tk,
+                            (4, 8, 8))
+    qr, kr, vr, gr = (x.clone().requires_grad_() for x in (q, k, v, gate))
+    ref = O.torch_vsa(qr, kr, vr, vbs, vbs, tk, (4, 8, 8), gr, selected=sel.cpu().long())
+    ref.backward(do)
+    assert_parity(out, ref, what="out")
+    for a, e, n in ((qg, qr, "dq"), (kg, kr, "dk"), (vg, vr, "dv"), (gg, gr, "dgate")):
+        assert_parity(a.grad, e.grad, what=n)
+    # and the explicit-route loader against the oracle on the same route
+    so = vsa.mi355x_sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), sel, vbs.to(DEV),
+                                     block_size=(4, 8, 8))
+    assert_parity(so, O.sparse_attention(q, k, v, sel.cpu(), vbs, block_size=(4, 8, 8)),
+                  what="explicit-route out")

@@ -23,13 +23,13 @@ DEV = "cuda"
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
 
 def _run(q, k, v, sel, vbs, be, do):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     leaves = [t.clone().requires_grad_() for t in (q, k, v)]
     out = M.mi355x_sparse_attention(*leaves, sel, vbs, block_size=(1, 1, be))
     grads = torch.autograd.grad(out, leaves, do)
@@ -69,7 +69,7 @@ def test_long_route_equals_short_route(be, H, D, nb, n_real):
 def _order_case(H, nb, be, D, hot):
     """Inputs for the dK/dV dispatch-order checks: `hot` key blocks chosen by
     every query block (a skewed route), the other slots spread uniformly."""
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     g = torch.Generator().manual_seed(nb * 7 + hot)
     S, tk = nb * be, 4
     q, k, v, do = (torch.randn(1, H, S, D, generator=g).to(torch.bfloat16).to(DEV)
@@ -79,7 +79,7 @@ def _order_case(H, nb, be, D, hot):
     sel = torch.cat([torch.arange(hot).expand(1, H, nb, hot), rest], -1).to(torch.int32).to(DEV)
     vbs = torch.full((nb,), be, dtype=torch.int32, device=DEV)
     scale = 1.0 / math.sqrt(D)
-    out, lse = M.sparse_forward(q, k, v, sel, vbs, be, scale)
+    out, lse, _ = M.sparse_forward(q, k, v, sel, vbs, be, scale)
     delta, _, _ = M.backward_prep(out, do, be)
     inv, off, cnt = M.invert_routes(sel, nb)
     return M, q, k, v, do, lse, delta, sel, vbs, inv, off, cnt, scale, tk
@@ -88,7 +88,7 @@ def _order_case(H, nb, be, D, hot):
 @pytest.mark.parametrize("H,nb,be,D,hot", [(4, 160, 64, 64, 2), (2, 60, 256, 128, 1),
                                            (3, 40, 128, 256, 2), (16, 160, 256, 128, 0)])
 def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
-    from vsa import _lib
+    from vsa_mi355x import _lib
     M, q, k, v, do, lse, delta, sel, vbs, inv, off, cnt, scale, tk = _order_case(H, nb, be, D, hot)
     S = nb * be
     order = M.dkdv_tile_order(cnt, H, S, D, be)

@@ -27,7 +27,7 @@ CASES = [((1, 1, 16), 64, 8, 3, "full"), ((3, 3, 3), 32, 6, 2, "token"),
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
@@ -44,7 +44,7 @@ def _check(a, e, what, max_abs=2e-2, rel_l2=1e-2):
 
 @pytest.mark.parametrize("block,D,nb,topk,gate_kind", CASES)
 def test_padded_shapes_match_oracle(block, D, nb, topk, gate_kind):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     be = math.prod(block)
     B, H, S = 1, 2, be * nb
     g = torch.Generator(device=DEV).manual_seed(be * 1000 + D)
@@ -76,7 +76,7 @@ def test_padded_shapes_match_oracle(block, D, nb, topk, gate_kind):
 
 @pytest.mark.parametrize("be,D", [(16, 64), (100, 40), (64, 96)])
 def test_padded_explicit_route_matches_oracle(be, D):
-    from vsa import mi355x as M
+    from vsa_mi355x import mi355x as M
     B, H, nb, topk = 1, 2, 7, 3
     S = be * nb
     g = torch.Generator(device=DEV).manual_seed(be + D)

@@ -21,13 +21,13 @@ SHAPES = [((2, 6, 6), (2, 3, 3)), ((3, 5, 5), (2, 4, 4)), ((5, 7, 9), (4, 4, 4))
 def _gpu_only():
     if not torch.cuda.is_available():
         pytest.skip("needs an MI355X")
-    from vsa import _lib
+    from vsa_mi355x import _lib
     _lib.load()
     yield
 
 
 def _meta(shape, ts, device="cuda"):
-    from vsa import tiling
+    from vsa_mi355x import tiling
     return tiling.build_vsa_metadata(shape, ts, device=device)
 
 
@@ -50,7 +50,7 @@ def test_metadata_bit_exact(shape, ts, device):
                                          ((2, 5), torch.float16), ((4, 64), torch.bfloat16),
                                          ((7,), torch.int32)])
 def test_tile_untile_bit_exact(shape, ts, trail, dtype):
-    from vsa import tiling
+    from vsa_mi355x import tiling
     meta = _meta(shape, ts)
     ref = TO.build_vsa_metadata(shape, ts)
     S = math.prod(shape)
@@ -75,7 +75,7 @@ def test_tile_untile_bit_exact(shape, ts, trail, dtype):
 
 
 def test_reference_kats_on_gpu():
-    from vsa import tiling
+    from vsa_mi355x import tiling
     # tests/test_common.py:194-209
     meta = _meta((2, 6, 6), (2, 3, 3))
     seq = 2 * 6 * 6
@@ -93,7 +93,7 @@ def test_reference_kats_on_gpu():
 
 @pytest.mark.parametrize("shape,ts", [((3, 5, 5), (2, 4, 4)), ((5, 7, 9), (4, 4, 4))])
 def test_gradients_match_oracle_autograd(shape, ts):
-    from vsa import tiling
+    from vsa_mi355x import tiling
     meta = _meta(shape, ts)
     ref = TO.build_vsa_metadata(shape, ts)
     S = math.prod(shape)
@@ -118,7 +118,7 @@ def test_gradients_match_oracle_autograd(shape, ts):
 
 def test_full_size_c3_latent():
     # a 20 x 32 x 64 latent (40,960 tokens) in (4, 8, 8) tiles: the c3 sequence
-    from vsa import tiling
+    from vsa_mi355x import tiling
     shape, ts = (20, 32, 64), (4, 8, 8)
     meta = _meta(shape, ts)
     ref = TO.build_vsa_metadata(shape, ts)
@@ -137,8 +137,8 @@ def test_full_size_c3_latent():
 
 def test_tile_vsa_untile_chain_matches_oracle():
     # DiT usage: raster [B, S, H, D] -> tile -> [B, H, S_pad, D] -> mi355x_vsa -> untile
-    from vsa import tiling
-    from vsa import mi355x as M
+    from vsa_mi355x import tiling
+    from vsa_mi355x import mi355x as M
     shape, ts = (3, 10, 12), (2, 4, 8)       # partial tiles in every direction, be = 64
     meta = _meta(shape, ts)
     ref = TO.build_vsa_metadata(shape, ts)
