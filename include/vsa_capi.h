@@ -53,7 +53,8 @@ enum vsa_status {
   VSA_ERR_SHAPE = -2,       /* sizes inconsistent or out of range */
   VSA_ERR_DTYPE = -3,       /* dtype not supported by this entry point */
   VSA_ERR_UNSUPPORTED = -4, /* (block_elements, head_dim) pair has no kernel */
-  VSA_ERR_LAUNCH = -5       /* the HIP launch itself failed */
+  VSA_ERR_LAUNCH = -5,      /* the HIP launch itself failed */
+  VSA_ERR_TOO_LARGE = -6    /* beyond the static scratch of a no-allocation entry point */
 };
 
 /* Text for a status code (static storage). */
@@ -207,6 +208,30 @@ int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v, const void*
                         int64_t bh, int64_t sq, int64_t skv, int32_t head_dim,
                         int32_t block_elements, int32_t topk, float scale,
                         int32_t* tile_order, int32_t dtype, void* stream);
+
+/*
+ * vsa_sparse_bwd_dkdv without a caller workspace: same arguments and results,
+ * minus tile_order.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The tile order and scheduling
+ * counters that vsa_dkdv_tile_order would write into a caller buffer live in
+ * a file-scope device array of 1 MiB (262,144 int32) per GPU, held until the
+ * process ends; the call writes the order there and then runs the dK/dV
+ * kernel, allocating nothing.  Sizes whose order needs more than the array
+ * (8 * ceil(tiles / 8) + 16 > 262,144 entries, tiles as in
+ * vsa_dkdv_tile_order) return VSA_ERR_TOO_LARGE.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams, or two host
+ * threads) race and must be serialised by the caller.  fp32 inputs need no
+ * workspace and run as vsa_sparse_bwd_dkdv with tile_order = NULL.
+ */
+int vsa_sparse_bwd_dkdv_noalloc(const void* q, const void* k, const void* v, const void* dout,
+                                const float* lse, const float* delta, const int32_t* counts,
+                                const int32_t* offsets, const int32_t* inverse,
+                                const int32_t* kv_vbs, void* dk, void* dv,
+                                const void* d_k_c, const void* d_v_c,
+                                int64_t bh, int64_t sq, int64_t skv, int32_t head_dim,
+                                int32_t block_elements, int32_t topk, float scale,
+                                int32_t dtype, void* stream);
 
 /*
  * Tile-layout metadata for a (T, H, W) latent grid and (ts, hs, ws) tiles, in

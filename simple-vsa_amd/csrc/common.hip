@@ -370,6 +370,8 @@ extern "C" const char* vsa_status_string(int status) {
     case VSA_ERR_DTYPE: return "dtype not supported by this entry point";
     case VSA_ERR_UNSUPPORTED: return "no kernel for this (block_elements, head_dim) pair";
     case VSA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case VSA_ERR_TOO_LARGE:
+      return "the sizes need more than the library's static scratch (no-allocation entry point)";
     default: return "unknown status";
   }
 }

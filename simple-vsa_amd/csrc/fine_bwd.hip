@@ -12,6 +12,7 @@
 //   S^T  = K Q^T,  dP^T = V dO^T,  dS^T = P^T (dP^T - delta),  dQ^T += K^T dS^T
 // dK/dV, per wave (32 keys) and 32-query sub-tile of an in-edge query block:
 //   S = Q K^T,  dP = dO V^T,  dS = P (dP - delta),  dV^T += dO^T P,  dK^T += Q^T dS
+#include <mutex>
 #include <type_traits>
 
 #include "fine_f32.h"
@@ -1160,4 +1161,71 @@ extern "C" int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v,
   VSA_DISPATCH_MFMA(dtype, T, { VSA_BWD_SHAPES(VSA_DKDV_CASE) });
 #undef VSA_DKDV_CASE
   return VSA_ERR_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// dK/dV without a caller workspace.  The tile order and scheduling counters
+// live in a file-scope device array: one copy per GPU, held until the process
+// ends.  Host code never passes the array's name to a kernel (on the host it
+// is only a stand-in for the symbol): each device's address comes from
+// hipGetSymbolAddress, resolved once per device with that device current.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchInts = 1 << 18;  // 1 MiB of int32
+static __device__ __align__(256) int32_t scratch[kNoAllocScratchInts];
+
+namespace {
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[64] = {nullptr};
+
+// The current device's copy of `scratch` (nullptr if it cannot be resolved).
+int32_t* device_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return nullptr;
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int vsa_sparse_bwd_dkdv_noalloc(const void* q, const void* k, const void* v,
+                                           const void* dout, const float* lse,
+                                           const float* delta, const int32_t* counts,
+                                           const int32_t* offsets, const int32_t* inverse,
+                                           const int32_t* kv_vbs, void* dk, void* dv,
+                                           const void* d_k_c, const void* d_v_c, int64_t bh,
+                                           int64_t sq, int64_t skv, int32_t D, int32_t be,
+                                           int32_t topk, float scale, int32_t dtype,
+                                           void* stream) {
+  if (dtype == VSA_F32)  // the fp32 kernels use no scheduling workspace
+    return vsa_sparse_bwd_dkdv(q, k, v, dout, lse, delta, counts, offsets, inverse, kv_vbs, dk,
+                               dv, d_k_c, d_v_c, bh, sq, skv, D, be, topk, scale, nullptr, dtype,
+                               stream);
+  if (dtype != VSA_BF16 && dtype != VSA_F16) return VSA_ERR_DTYPE;
+  // the checks of vsa_sparse_bwd_dkdv, made before the order kernel launches
+  if (!q || !k || !v || !dout || !lse || !delta || !counts || !offsets || !inverse || !kv_vbs ||
+      !dk || !dv)
+    return VSA_ERR_NULL;
+  if ((d_k_c == nullptr) != (d_v_c == nullptr)) return VSA_ERR_NULL;
+  if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
+      sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
+    return VSA_ERR_SHAPE;
+  DkvGeometry g;
+  if (!dkdv_geometry(D, be, skv, g)) return VSA_ERR_UNSUPPORTED;
+  const int64_t tiles = bh * g.tph * g.nsplit;
+  const int64_t order_len = 8 * ((tiles + 7) / 8) + 16;
+  if (tiles > (1LL << 30) || order_len > kNoAllocScratchInts) return VSA_ERR_TOO_LARGE;
+  int32_t* order = device_scratch();
+  if (order == nullptr) return VSA_ERR_LAUNCH;
+  // the order call rewrites every entry the dK/dV kernel reads and zeroes its
+  // counters, so the previous call's contents do not matter
+  int rc = vsa_dkdv_tile_order(counts, order, order_len, bh, skv, D, be, stream);
+  if (rc != VSA_OK) return rc;
+  return vsa_sparse_bwd_dkdv(q, k, v, dout, lse, delta, counts, offsets, inverse, kv_vbs, dk,
+                             dv, d_k_c, d_v_c, bh, sq, skv, D, be, topk, scale, order, dtype,
+                             stream);
 }

@@ -42,6 +42,8 @@ SIGNATURES = {
     "vsa_dkdv_tile_order": [_P, _P, _I64, _I64, _I64, _I32, _I32, _P],
     "vsa_sparse_bwd_dkdv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                             _I64, _I32, _I32, _I32, _F, _P, _I32, _P],
+    "vsa_sparse_bwd_dkdv_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                    _I64, _I64, _I32, _I32, _I32, _F, _I32, _P],
     "vsa_tile_metadata": [_I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P],
     "vsa_rows_move": [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _P,
                       _I64, _P],

@@ -25,7 +25,7 @@ def test_header_declares_the_expected_entry_points():
     names = _declared_symbols()
     for must in ("vsa_pool_qkv", "vsa_coarse_fwd", "vsa_topk", "vsa_csr_build", "vsa_sparse_fwd",
                  "vsa_bwd_prep", "vsa_coarse_bwd", "vsa_sparse_bwd_dq", "vsa_sparse_bwd_dkdv",
-                 "vsa_dkdv_tile_order",
+                 "vsa_dkdv_tile_order", "vsa_sparse_bwd_dkdv_noalloc",
                  "vsa_status_string", "vsa_version"):
         assert must in names
 
@@ -70,6 +70,18 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, p, p, 3, 3,
                               4, 64, 64, 128, 64, 1, 0.1, 0, None) == -2
     assert lib.vsa_bwd_prep(p, p, p, p, 3, 0, p, p, p, 4, 64, 128, 64, 0, None) == -2
+    # no-allocation dK/dV: sizes whose tile order exceeds the 1 MiB static scratch
+    # (8 * ceil(tiles / 8) + 16 > 262144 int32) are rejected before any launch
+    noalloc = [p] * 14
+    assert lib.vsa_sparse_bwd_dkdv_noalloc(*noalloc, 64, 1024, 128 * 4096, 128, 256, 8, 0.1,
+                                           0, None) == -6
+    assert "static scratch" in _lib.status_string(-6)
+    assert lib.vsa_sparse_bwd_dkdv_noalloc(*noalloc, 1, 1024, 1024, 128, 96, 8, 0.1,
+                                           0, None) == -2              # 1024 % 96
+    assert lib.vsa_sparse_bwd_dkdv_noalloc(*noalloc, 1, 1024, 1024, 128, 256, 8, 0.1,
+                                           7, None) == -3              # no dtype 7
+    assert lib.vsa_sparse_bwd_dkdv_noalloc(*([None] + noalloc[1:]), 1, 1024, 1024, 128, 256, 8,
+                                           0.1, 0, None) == -1
     # tiling entry points validate before launching
     assert lib.vsa_tile_metadata(0, 4, 4, 2, 2, 2, p, p, p, p, None) == -2
     assert lib.vsa_tile_metadata(4, 4, 4, 2, 2, 2, None, p, p, p, None) == -1
