@@ -41,23 +41,34 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor
 
-# Which independent check pins each function (tests/test_oracle.py holds them).
+# Which independent check pins each function (tests/test_oracle.py and
+# tests/test_oracle_rounding.py hold them).  No golden vectors of the reference
+# exist (its tests hold none), so every pin is a known answer from the
+# reference's own tests, a textbook identity or a brute force; each check also
+# catches at least one planted mistake.
 PINNING = {
     "as_block_elements": "closed form; int -> cube (tests/test_torch_vsa.py:59-72 KAT)",
     "valid_token_mask": "closed form pos < vbs; brute force loop",
     "block_mean": "KAT [2.0, 2.0] ignoring padding 999 (tests/test_common.py:81-88); "
-                  "explicit per-block mean (tests/test_common.py:63-78)",
+                  "explicit per-block mean (tests/test_common.py:63-78); bf16 / fp16: "
+                  "T(fp64 sum / count) brute force (planted: fp32 result, padded divisor)",
     "validate_vsa_inputs": "error-text KATs (tests/test_torch_vsa.py:112-130)",
-    "coarse_branch_compact": "fp32: equals F.scaled_dot_product_attention on pooled tokens; "
-                             "compact == expanded (tests/test_common.py:91-112); "
-                             "bf16 rounding points: golden vectors from the reference",
+    "coarse_branch_compact": "fp64: equals F.scaled_dot_product_attention on pooled tokens; "
+                             "compact == expanded (tests/test_common.py:91-112); bf16 / fp16: "
+                             "scores T(T(dot) * scale), P = T(softmax), out_c = T(P v_c) by fp64 "
+                             "brute force from the T operands (planted: fp32 scores, fp32 "
+                             "softmax, fp32 out_c, one rounding of the scores)",
     "topk_reference": "brute-force full sort; torch.topk on tie-free rows; exactly tk per row "
                       "(tests/test_common.py:165-172)",
     "video_sparse_attn": "topk = Kb with full blocks == SDPA (tests/test_common.py:115-130); "
-                         "gate 0 / gate 2 (tests/test_common.py:145-162); out == compress + sparse",
+                         "gate 0 / gate 2 (tests/test_common.py:145-162); out == compress + "
+                         "sparse; bf16 / fp16 route == torch.topk of the brute-force T scores, "
+                         "ties included (planted: routing on fp32 scores)",
     "torch_vsa": "== masked-fill video_sparse_attn at 1e-5, full / padded / gate / int block "
                  "(tests/test_torch_vsa.py:12-72); unselected blocks get gradient (89-109); "
-                 "fp64 gradcheck",
+                 "fp64 gradcheck; bf16 / fp16 output == T(float(out_c) * float(gate) + out_s) "
+                 "by fp64 brute force (planted: out_c kept in fp32); fp32 gather measured "
+                 "against the T gather of torch_impl.py and fp64 on a Zipf hot-key route",
     "sparse_attention_reference": "hot-KV dense per-block softmax (tests/test_helion_vsa.py:332-403); "
                                   "all blocks selected == SDPA; LSE2 == log2 sum exp2 brute force",
     "sparse_attention": "fp64 gradcheck; == torch_vsa fine branch with the same route",

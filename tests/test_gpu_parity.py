@@ -445,3 +445,36 @@ def test_registry_loader_full_op_parity(tmp_path, monkeypatch):
                                      block_size=(4, 8, 8))
     assert_parity(so, O.sparse_attention(q, k, v, sel.cpu(), vbs, block_size=(4, 8, 8)),
                   what="explicit-route out")
+
+
+def test_route_agrees_with_the_oracles_own_topk_end_to_end():
+    """End-to-end routing without the route override: the GPU's Top-K against
+    torch.topk of the oracle's own bf16 scores (torch_impl.py:85), at the
+    north-star block statistics (be 256, 160 key blocks, topk 20).  Rows whose
+    scores match bit for bit and whose 20th and 21st scores are not tied must
+    select the same set; tied rows may differ only in the tie order (the GPU
+    takes the smaller block id, torch.topk's order is implementation-defined)."""
+    from vsa_mi355x import mi355x as M
+    g = torch.Generator().manual_seed(67)
+    be, nb, h, d, tk = 256, 160, 2, 128, 20
+    q, k, v = (_randn((1, h, nb * be, d), g, torch.bfloat16) for _ in range(3))
+    vbs = torch.full((nb,), be)
+    scores, sel = M.mi355x_route(*_gpu(q, k, v), vbs.to(DEV), vbs.to(DEV), tk, (4, 8, 8))
+    o_scores, _ = O.coarse_branch_compact(q, k, v, vbs, vbs, be, d ** -0.5)
+    o_sel = o_scores.topk(tk, dim=-1).indices.sort(-1).values
+    srt = o_scores.sort(dim=-1, descending=True).values
+    tied = srt[..., tk - 1] == srt[..., tk]
+    same_scores = (scores.cpu() == o_scores.float()).all(-1)
+    agree = (sel.cpu().long() == o_sel).all(-1)
+    print(f"route agreement: all rows {agree.float().mean():.4f}, untied rows "
+          f"{agree[~tied].float().mean():.4f}; tied rows {tied.float().mean():.4f}; rows with "
+          f"bit-identical scores {same_scores.float().mean():.4f}", flush=True)
+    assert agree[~tied & same_scores].all()
+    assert same_scores.float().mean() > 0.95
+    # on tied rows the selected sets share every block above the tied value
+    for i in torch.nonzero(tied & same_scores & ~agree).tolist():
+        row = o_scores[tuple(i)].float()
+        kth = srt[tuple(i)][tk - 1].float()
+        above = set(torch.nonzero(row > kth).flatten().tolist())
+        assert above <= set(sel.cpu()[tuple(i)].tolist())
+        assert all(row[j] >= kth for j in sel.cpu()[tuple(i)].tolist())

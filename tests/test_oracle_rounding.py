@@ -1,0 +1,312 @@
+"""Pins the oracle's low-precision rounding points by brute force.
+
+The reference computes the coarse branch in the input dtype T on purpose, so
+that Top-K routing sees the same scores FastVideo does (common.py:159-166):
+``scores = T(T(q_c k_c^T) * scale)``, ``P = T(softmax(scores))``,
+``out_c = T(P v_c)``; block means are ``T(fp32 sum / count)`` (common.py:55-82)
+and ``out_c`` is promoted only at the combine,
+``out = T(float(out_c) * float(gate) + out_s)`` (torch_impl.py:108-113).
+
+Each check below recomputes one of these from the T-rounded operands in fp64
+and rounds to T with torch's own round-to-nearest-even cast.  An fp32 sum
+taken in another order can land on the other side of a rounding boundary, so
+a value may differ from the brute force by one ulp of T; a wrong rounding point
+makes many values differ, so at least 99 % must match exactly (measured:
+every value matches on these inputs).  Planted mistakes -- routing on fp32
+scores, ``out_c`` kept in fp32, softmax kept in fp32, one rounding instead of
+two for the scores -- must each fail one of the checks.
+
+The last test backs a documented deviation of the oracle from torch_impl.py
+with data: it gathers key/value blocks from fp32 copies, so the gradient of a
+key block shared by many query blocks accumulates in fp32 (torch_impl.py
+gathers in T, so autograd accumulates those gradients in T).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import vsa_oracle as O
+
+LOW = [torch.bfloat16, torch.float16]
+
+
+# ---------------------------------------------------------------------------
+# brute force in fp64 from T-rounded operands
+# ---------------------------------------------------------------------------
+
+def _t(x64, dtype):
+    """Round fp64 values to T (round to nearest even) and back to fp64."""
+    return x64.to(dtype).double()
+
+
+def brute_block_mean(x, vbs, be):
+    b, h, s, d = x.shape
+    nb = s // be
+    xb = x.double().reshape(b, h, nb, be, d)
+    out = torch.zeros(b, h, nb, d, dtype=torch.float64)
+    for n in range(nb):
+        c = int(vbs[n])
+        if c > 0:
+            out[:, :, n] = xb[:, :, n, :c].sum(2) / c
+    return _t(out, x.dtype)
+
+
+def brute_coarse(qc, kc, vc, scale):
+    """(scores, P, out_c) with every rounding point of common.py:164-166."""
+    t = qc.dtype
+    dot = _t(qc.double() @ kc.double().transpose(-2, -1), t)
+    scores = _t(dot * float(torch.tensor(scale, dtype=torch.float32)), t)
+    p = _t(torch.softmax(scores, dim=-1), t)
+    out_c = _t(p @ vc.double(), t)
+    return scores, p, out_c
+
+
+def assert_rounded_like(got, exp, dtype, what, exact_frac=0.99, slack=0.0):
+    """At most one ulp of T off everywhere (plus ``slack``, an absolute bound on
+    fp32 arithmetic error where the value cancels to near zero), and exact on
+    at least ``exact_frac`` of the values."""
+    assert got.dtype == dtype, f"{what}: stored as {got.dtype}, not {dtype}"
+    fi = torch.finfo(dtype)
+    spacing = torch.clamp(exp.abs(), min=fi.tiny) * fi.eps
+    err = (got.double() - exp.double()).abs()
+    worst = ((err - slack) / spacing).max().item()
+    assert worst <= 1.0, f"{what}: {worst:.2f} ulp off"
+    frac = (err == 0).double().mean().item()
+    assert frac >= exact_frac, f"{what}: only {frac:.4f} of the values match exactly"
+
+
+def _pooled_case(dtype, seed, be=16, nb=12, h=3, d=96, scale_in=1.0):
+    """Inputs with ragged blocks; head_dim 96, so the scale 1/sqrt(96) is not a
+    power of two and T(T(dot) * scale) differs from T(dot * scale)."""
+    g = torch.Generator().manual_seed(seed)
+    shape = (1, h, nb * be, d)
+    q, k, v = ((torch.randn(shape, generator=g) * scale_in).to(dtype) for _ in range(3))
+    vbs = torch.full((nb,), be)
+    vbs[3], vbs[7] = be - 5, 1
+    return q, k, v, vbs, be, d ** -0.5
+
+
+# ---------------------------------------------------------------------------
+# the oracle's rounding points
+# ---------------------------------------------------------------------------
+
+def check_block_mean(fn, dtype):
+    q, _, _, vbs, be, _ = _pooled_case(dtype, 1)
+    assert_rounded_like(fn(q, vbs, be), brute_block_mean(q, vbs, be), dtype, "block_mean")
+
+
+def check_coarse(fn, dtype, seed=2):
+    q, k, v, vbs, be, scale = _pooled_case(dtype, seed)
+    scores, out_c = fn(q, k, v, vbs, vbs, be, scale)
+    qc, kc, vc = (O.block_mean(t, vbs, be) for t in (q, k, v))
+    e_scores, _, e_out = brute_coarse(qc, kc, vc, scale)
+    assert_rounded_like(scores, e_scores, dtype, "scores")
+    assert_rounded_like(out_c, e_out, dtype, "out_c")
+
+
+def check_routing(fn, dtype, seed=3, topk=20):
+    """The route of the masked-fill oracle is torch.topk (the reference's call,
+    common.py:85-94) of the T-rounded brute-force scores, tie order included.
+    The pooled inputs are small, so many rows tie at the k-th score in T: an
+    fp32 route agrees with the T route wherever T keeps the k-th and (k+1)-th
+    scores apart (rounding is monotonic), so only the tied rows tell the two
+    apart."""
+    # 160 key blocks and topk 20 as at the north-star shape: the 20th and 21st
+    # scores are close, so T's rounding ties them in some rows
+    q, k, v, vbs, be, scale = _pooled_case(dtype, seed, be=4, nb=160, h=16, d=128)
+    real = O.coarse_branch_compact
+    try:
+        O.coarse_branch_compact = fn
+        _, aux = O.video_sparse_attn(q, k, v, vbs, vbs, topk, block_size=(1, 1, be),
+                                     return_aux=True)
+    finally:
+        O.coarse_branch_compact = real
+    qc, kc, vc = (O.block_mean(t, vbs, be) for t in (q, k, v))
+    e_scores, _, _ = brute_coarse(qc, kc, vc, scale)
+    srt = e_scores.sort(dim=-1, descending=True).values
+    tied = srt[..., topk - 1] == srt[..., topk]
+    assert tied.sum() >= 10, "the case must tie at the k-th score in some rows"
+    ids = e_scores.to(dtype).topk(topk, dim=-1).indices
+    exp_mask = torch.zeros_like(aux["block_mask"]).scatter_(-1, ids, True)
+    same = (aux["block_mask"] == exp_mask).all(-1)
+    assert same.all(), f"{int((~same).sum())} routed rows differ ({int(tied.sum())} tied rows)"
+
+
+def check_combine(dtype, seed=4):
+    """A T-dtype torch_vsa output is T(float(out_c) * float(gate) + out_s)."""
+    q, k, v, vbs, be, scale = _pooled_case(dtype, seed)
+    g = torch.Generator().manual_seed(seed + 100)
+    gate = torch.rand(q.shape, generator=g).to(dtype)
+    qc, kc, vc = (O.block_mean(t, vbs, be) for t in (q, k, v))
+    scores, _, out_c = brute_coarse(qc, kc, vc, scale)
+    # one route for both sides (torch.topk's order among tied scores is open)
+    sel = torch.from_numpy(O.topk_reference(scores, 3)).long()
+    out = O.torch_vsa(q, k, v, vbs, vbs, 3, (1, 1, be), gate, selected=sel)
+    out_s, _ = O.sparse_attention_reference(q.double(), k.double(), v.double(), sel, vbs, be,
+                                            scale)
+    b, h, s, d = q.shape
+    out_c_tok = out_c[:, :, :, None, :].expand(b, h, s // be, be, d).reshape(b, h, s, d)
+    exp = _t(out_c_tok * gate.double() + out_s, dtype)
+    # the oracle's fine branch runs in fp32: where out_c * gate + out_s cancels,
+    # its error (a few fp32 ulps of the O(1) terms) exceeds T's spacing
+    assert_rounded_like(out, exp, dtype, "torch_vsa out", slack=1e-6)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+def test_block_mean_rounding_point(dtype):
+    check_block_mean(O.block_mean, dtype)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+def test_coarse_branch_rounding_points(dtype):
+    check_coarse(O.coarse_branch_compact, dtype)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+def test_routing_uses_t_rounded_scores(dtype):
+    check_routing(O.coarse_branch_compact, dtype)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+def test_combine_promotes_out_c_only_at_the_combine(dtype):
+    check_combine(dtype)
+
+
+# ---------------------------------------------------------------------------
+# planted mistakes: each one must fail a check above
+# ---------------------------------------------------------------------------
+
+def _pooled(q, k, v, vbs, qvbs, be):
+    return O.block_mean(q, qvbs, be), O.block_mean(k, vbs, be), O.block_mean(v, vbs, be)
+
+
+def mistake_fp32_scores(q, k, v, vbs, qvbs, be, scale):
+    """Scores, softmax and out_c in fp32 (routing on fp32 scores)."""
+    qc, kc, vc = (t.float() for t in _pooled(q, k, v, vbs, qvbs, be))
+    scores = qc @ kc.transpose(-2, -1) * scale
+    out_c = torch.softmax(scores, -1) @ vc
+    return scores, out_c.to(q.dtype)
+
+
+def mistake_fp32_out_c(q, k, v, vbs, qvbs, be, scale):
+    """Scores and softmax in T, but out_c kept in fp32."""
+    qc, kc, vc = _pooled(q, k, v, vbs, qvbs, be)
+    scores = torch.matmul(qc, kc.transpose(-2, -1).contiguous()) * scale
+    p = torch.softmax(scores, -1)
+    return scores, p.float() @ vc.float()
+
+
+def mistake_fp32_softmax(q, k, v, vbs, qvbs, be, scale):
+    """Scores in T, softmax kept in fp32, out_c rounded to T."""
+    qc, kc, vc = _pooled(q, k, v, vbs, qvbs, be)
+    scores = torch.matmul(qc, kc.transpose(-2, -1).contiguous()) * scale
+    p = torch.softmax(scores.float(), -1)
+    return scores, (p @ vc.float()).to(q.dtype)
+
+
+def mistake_single_rounding(q, k, v, vbs, qvbs, be, scale):
+    """Scores rounded once, T(dot * scale), instead of T(T(dot) * scale)."""
+    qc, kc, vc = _pooled(q, k, v, vbs, qvbs, be)
+    scores = (qc.float() @ kc.float().transpose(-2, -1) * scale).to(q.dtype)
+    return scores, torch.matmul(torch.softmax(scores, -1), vc)
+
+
+def mistake_fp32_block_mean(x, vbs, be):
+    """Block mean left in fp32."""
+    return O.block_mean(x.float(), vbs, be)
+
+
+def mistake_mean_over_padded_volume(x, vbs, be):
+    """Block mean divided by the padded volume instead of the valid count."""
+    b, h, s, d = x.shape
+    nb = s // be
+    valid = O.valid_token_mask(vbs, be).view(1, 1, nb, be, 1)
+    return ((x.float().reshape(b, h, nb, be, d) * valid).sum(3) / be).to(x.dtype)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+@pytest.mark.parametrize("mistake", [mistake_fp32_scores, mistake_fp32_out_c,
+                                     mistake_fp32_softmax, mistake_single_rounding])
+def test_planted_coarse_mistakes_are_caught(dtype, mistake):
+    with pytest.raises(AssertionError):
+        check_coarse(mistake, dtype)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+def test_planted_fp32_routing_changes_routed_rows(dtype):
+    with pytest.raises(AssertionError):
+        check_routing(mistake_fp32_scores, dtype)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+@pytest.mark.parametrize("mistake", [mistake_fp32_block_mean, mistake_mean_over_padded_volume])
+def test_planted_block_mean_mistakes_are_caught(dtype, mistake):
+    with pytest.raises(AssertionError):
+        check_block_mean(mistake, dtype)
+
+
+@pytest.mark.parametrize("dtype", LOW)
+def test_planted_fp32_out_c_at_the_combine_is_caught(dtype, monkeypatch):
+    monkeypatch.setattr(O, "coarse_branch_compact", mistake_fp32_out_c)
+    with pytest.raises(AssertionError):
+        check_combine(dtype)
+
+
+# ---------------------------------------------------------------------------
+# the fp32 gather: the oracle's one deliberate deviation from torch_impl.py
+# ---------------------------------------------------------------------------
+
+def _fine_grads(q, k, v, sel, vbs, be, scale, do, gather_in_t):
+    """(dq, dk, dv) of the explicit-route fine branch; with gather_in_t the key
+    and value blocks are gathered in T and promoted afterwards, as
+    torch_impl.py:86-87 does, else gathered from fp32 copies as the oracle does."""
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    qq, kk, vv = leaves
+    if gather_in_t:
+        b, h, s, d = qq.shape
+        qb, tk = s // be, sel.shape[-1]
+        sk = O._gather_blocks(kk, sel, be).float().reshape(b, h, qb, tk * be, d)
+        sv = O._gather_blocks(vv, sel, be).float().reshape(b, h, qb, tk * be, d)
+        valid = O.valid_token_mask(vbs, be)[sel].reshape(b, h, qb, 1, tk * be)
+        sc = torch.matmul(qq.float().reshape(b, h, qb, be, d), sk.transpose(-2, -1)) * scale
+        p = torch.softmax(sc.masked_fill(~valid, float("-inf")), dim=-1)
+        out = torch.matmul(p, sv).reshape(b, h, s, d)
+    else:
+        out, _ = O.sparse_attention_reference(qq, kk, vv, sel, vbs, be, scale)
+    out.backward(do)
+    return [x.grad.double() for x in leaves]
+
+
+def test_fp32_gather_against_t_gather_on_a_hot_key_route():
+    """Zipf(1.2) routes: a few key blocks are chosen by most query blocks (the
+    hottest by 191 of 192).  The T-gather's key/value gradients are several
+    times further from fp64 than the fp32-gather's (measured here, relative L2:
+    dk 7.8e-3 vs 1.7e-3, dv 7.7e-3 vs 1.7e-3); the query gradient does not
+    accumulate across query blocks and is the same for both."""
+    g = torch.Generator().manual_seed(5)
+    rng = np.random.default_rng(5)
+    be, nb, h, d, tk = 16, 96, 2, 32, 12
+    shape = (1, h, nb * be, d)
+    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
+    p = 1.0 / np.arange(1, nb + 1) ** 1.2
+    p /= p.sum()
+    perm = rng.permutation(nb)
+    sel = torch.tensor(np.stack([perm[rng.choice(nb, tk, replace=False, p=p)]
+                                 for _ in range(h * nb)]).reshape(1, h, nb, tk))
+    counts = np.bincount(sel.flatten().numpy(), minlength=nb)
+    assert counts.max() >= 60                      # hot key blocks, tens of in-edges
+    vbs = torch.full((nb,), be)
+    scale = d ** -0.5
+    exact = _fine_grads(q.double(), k.double(), v.double(), sel, vbs, be, scale, do.double(),
+                        False)
+    f32 = _fine_grads(q, k, v, sel, vbs, be, scale, do.float(), False)
+    lit = _fine_grads(q, k, v, sel, vbs, be, scale, do.float(), True)
+    rel = lambda a, e: ((a - e).norm() / e.norm()).item()
+    for i, name in ((1, "dk"), (2, "dv")):
+        e32, elit = rel(f32[i], exact[i]), rel(lit[i], exact[i])
+        assert e32 <= 4e-3, (name, e32)
+        assert elit >= 3 * e32, (name, e32, elit)
+    assert math.isclose(rel(f32[0], exact[0]), rel(lit[0], exact[0]), rel_tol=0.1)
