@@ -74,13 +74,49 @@ def _events_time(fn, iters):
     return start.elapsed_time(end) / iters
 
 
+def host_cpu():
+    """The host CPU the baseline runs on: model, logical CPUs of the machine and
+    of this process, and the physical cores among this process's CPUs."""
+    info = {"model": None, "os_cpu_count": os.cpu_count()}
+    try:
+        allowed = sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = list(range(os.cpu_count() or 1))
+    info["cpus_allowed"] = len(allowed)
+    cores, proc = {}, {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f.read().split("\n") + [""]:
+                if not ln.strip():
+                    if "processor" in proc:
+                        cores[int(proc["processor"])] = (proc.get("physical id", "0"),
+                                                         proc.get("core id", proc["processor"]))
+                        info["model"] = info["model"] or proc.get("model name")
+                    proc = {}
+                    continue
+                key, _, val = ln.partition(":")
+                proc[key.strip()] = val.strip()
+    except OSError:
+        pass
+    phys = {cores[c] for c in allowed if c in cores}
+    info["physical_cores_allowed"] = len(phys) if phys else len(allowed)
+    return info
+
+
 def cpu_baseline(heads: int = 8):
     """The CPU oracle (a restatement of torch_vsa) fwd+bwd on `heads` heads of
     the workload, one head at a time (heads are independent; one head's
-    fp32 intermediates are a few GB).  Returns (TFLOP/s, seconds, threads)."""
+    fp32 intermediates are a few GB), with one torch thread per physical core
+    this process may use (at most OMP_NUM_THREADS when that is set).
+    Returns (TFLOP/s, seconds, threads, host description)."""
     import torch
     sys.path.insert(0, ROOT)
     from oracle import vsa_oracle as O
+    host = host_cpu()
+    threads = host["physical_cores_allowed"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(max(1, threads))
     threads = torch.get_num_threads()
     B, S, D, topk = CFG["B"], CFG["S"], CFG["D"], CFG["topk"]
     be = math.prod(CFG["block"])
@@ -98,7 +134,7 @@ def cpu_baseline(heads: int = 8):
         torch.autograd.grad(out, (q, k, v, gate), do)
         total += time.perf_counter() - t0
     f = 3.5 * flops_fwd(B, heads, S, D, be, topk)
-    return f / total / 1e12, total, threads
+    return f / total / 1e12, total, threads, host
 
 
 def _zipf_routes(h, qb, kb, tk, s, seed=5):
@@ -257,6 +293,9 @@ def main():
     ap.add_argument("--kernels-only", action="store_true", help="skip the CPU baseline and summary")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy a 1 GiB buffer 3 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
+    ap.add_argument("--workload-steps", type=int, default=5,
+                    help="timed steps of each other BASELINE configuration (c2, c4, c5) "
+                         "reported under 'workloads' of the c3 line; 0 skips them")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of the workload timed on the CPU oracle (one at a time)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["tiling", "gate"], default="c3",
@@ -388,14 +427,30 @@ def main():
 
     F_total = 3.5 * F_fwd
     value = F_total / (ms_step * 1e-3) / 1e12
+    # the other BASELINE configurations, a few steps each, after c3's tensors are freed
+    workloads = None
+    if not args.kernels_only and args.workload_steps > 0:
+        del q, k, v, do, gate, qd, kd, vd, gd, out, lse, fine, delta, dq, dk, dv
+        torch.cuda.empty_cache()
+        workloads = {}
+        for key in ("c2", "c4", "c5"):
+            r = run_workload(key, args.workload_steps, 2)
+            workloads[key] = {n: r[n] for n in ("ms_fwd_bwd", "ms_fwd", "tflops_fwd_bwd",
+                                                "tflops_fwd", "pct_bf16_peak_fwd_bwd",
+                                                "peak_hbm_gib_beyond_inputs", "steps")}
+            torch.cuda.empty_cache()
     cpu = None
     if not (args.no_cpu or args.kernels_only):
-        cv, cs, cth = cpu_baseline(heads=args.cpu_heads)
+        cv, cs, cth, host = cpu_baseline(heads=args.cpu_heads)
         cpu = {"value": round(cv, 4), "unit": "TFLOP/s", "cores": cth, "kind": "port",
                "sample": f"oracle torch_vsa fwd+bwd, {args.cpu_heads} of {H} heads of the "
                          "workload, one head at a time "
                          f"(B=1,H=1,S={S},D={D},be={be},topk={topk}, bf16 inputs), "
-                         f"{cs:.1f} s wall, throughput in effective TFLOP/s"}
+                         f"{cs:.1f} s wall, throughput in effective TFLOP/s",
+               "host": {"cpu_model": host["model"], "os_cpu_count": host["os_cpu_count"],
+                        "cpus_allowed": host["cpus_allowed"],
+                        "physical_cores_allowed": host["physical_cores_allowed"],
+                        "torch_threads": cth}}
     line = {
         "metric": "VSA fwd+bwd ms & effective TFLOP/s (% bf16 MFMA peak) at 40k tokens, block 256",
         "value": round(value, 2),
@@ -420,6 +475,7 @@ def main():
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic},
         "kernels": kernels,
+        "workloads": workloads,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
