@@ -38,13 +38,17 @@ enum vsa_dtype { VSA_BF16 = 0, VSA_F16 = 1, VSA_F32 = 2 };
  * How compress_attn_weight is laid out: absent, [BH, Sq, D], [BH, Sq, 1], or
  * token-major [B, Sq, H, D] -- the gate producer's Linear output before its
  * per-head transpose (common.py:326-328), read and written in place; H is the
- * `gate_heads` argument and bh = b*H + h.
+ * `gate_heads` argument and bh = b*H + h.  The gate has the inputs' dtype,
+ * unless VSA_GATE_F32 is OR-ed into the mode: then it is fp32 beside bf16 /
+ * fp16 inputs (the reference promotes the gate with .float(), torch_impl.py:110,
+ * and keeps its gradient in the gate's dtype, fused_common.py:202-221).
  */
 enum vsa_gate_mode {
   VSA_GATE_NONE = 0,
   VSA_GATE_FULL = 1,
   VSA_GATE_PER_TOKEN = 2,
-  VSA_GATE_TOKEN_MAJOR = 3
+  VSA_GATE_TOKEN_MAJOR = 3,
+  VSA_GATE_F32 = 4          /* flag: the gate (and d_gate) are fp32 */
 };
 
 enum vsa_status {
@@ -121,6 +125,9 @@ int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
  *   fine_out = T(attn)   when out_c != NULL and fine_out != NULL: the fine
  *                        output the reference's fused path keeps as its own
  *                        tensor (triton_impl.py:408); vsa_bwd_prep takes it
+ * With VSA_GATE_F32 the combine runs as a second pass over the T-rounded fine
+ * output, out = T(out_c[block] * gate + T(attn)), as the reference's fused
+ * combine does (fused_common.py:175-199).
  *   lse[bh, q] = log2(sum_j exp2(scale*log2(e) * q.k_j))   (may be NULL)
  * block_elements in {64, 128, 256}; head_dim in {64, 128, 256}.
  */
@@ -140,7 +147,8 @@ int vsa_sparse_fwd(const void* q, const void* k, const void* v,
  *   delta[bh, q]   = sum_d fine_out * dout                           (fp32)
  *   d_out_c[bh, n] = T(sum_{t < be} T(dout * gate))     (if out_c != NULL)
  *   d_gate         = T(dout * out_c[block])  (per token: summed over d),
- * d_gate in the gate's own layout (token-major included).
+ * d_gate in the gate's own layout (token-major included) and dtype (fp32 with
+ * VSA_GATE_F32).
  */
 int vsa_bwd_prep(const void* fine_out, const void* dout, const void* out_c, const void* gate,
                  int32_t gate_mode, int32_t gate_heads, float* delta, void* d_out_c, void* d_gate,

@@ -200,17 +200,46 @@ __global__ __launch_bounds__(256) void csr_sort_kernel(const int32_t* __restrict
   }
 }
 
+// VEC consecutive gate values of element type G as fp32 (16-byte loads), and
+// the matching store of VEC values of G.
+template <typename G, int VEC>
+__device__ __forceinline__ void load_gate(const G* __restrict__ p, float* out) {
+  constexpr int N = VEC * (int)sizeof(G) / 16;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    u32x4 r = *reinterpret_cast<const u32x4*>(p + i * (16 / sizeof(G)));
+    const G* g = reinterpret_cast<const G*>(&r);
+#pragma unroll
+    for (int e = 0; e < 16 / (int)sizeof(G); ++e) out[i * (16 / sizeof(G)) + e] = Elem<G>::to_f(g[e]);
+  }
+}
+
+template <typename G, int VEC>
+__device__ __forceinline__ void store_gate(G* __restrict__ p, const float* v) {
+  constexpr int PER = 16 / (int)sizeof(G);
+#pragma unroll
+  for (int i = 0; i < VEC / PER; ++i) {
+    G g[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) g[e] = Elem<G>::from_f(v[i * PER + e]);
+    *reinterpret_cast<u32x4*>(p + i * PER) = *reinterpret_cast<const u32x4*>(g);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Backward preprocessing: one workgroup per (bh, query block).  delta is the
 // row sum of the fine output as the forward stored it in T times dout (the
 // reference's delta over its stored sparse output, triton_impl.py:598-700),
-// never a difference recovered from the rounded combined output.
+// never a difference recovered from the rounded combined output.  The gate
+// has element type G: T, or fp32 for an fp32 gate beside T inputs (its
+// gradient is then stored in fp32, as the reference stores it in the gate's
+// dtype, fused_common.py:202-221).
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename G>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const T* __restrict__ fine, const T* __restrict__ dout, const T* __restrict__ outc,
-    const T* __restrict__ gate, int gate_mode, int gate_heads, float* __restrict__ delta,
-    T* __restrict__ d_outc, T* __restrict__ d_gate, int qb, int D, int be) {
+    const G* __restrict__ gate, int gate_mode, int gate_heads, float* __restrict__ delta,
+    T* __restrict__ d_outc, G* __restrict__ d_gate, int qb, int D, int be) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float part[256 * VEC];
   const int64_t blk = blockIdx.x + (int64_t)blockIdx.y * qb;  // bh*qb + n
@@ -243,29 +272,25 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const T* g = reinterpret_cast<const T*>(&rd);
     float gv[VEC];
     if (gate_mode == 1 || gate_mode == 3) {
-      u32x4 rg = *reinterpret_cast<const u32x4*>(gate + goff);
-      const T* gg = reinterpret_cast<const T*>(&rg);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) gv[e] = Elem<T>::to_f(gg[e]);
+      load_gate<G, VEC>(gate + goff, gv);
     } else {
-      const float gs = gate_mode == 2 ? Elem<T>::to_f(gate[tok]) : 1.f;
+      const float gs = gate_mode == 2 ? Elem<G>::to_f(gate[tok]) : 1.f;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) gv[e] = gs;
     }
     float dl = 0.f, dg = 0.f;
-    T dgv[VEC];  // this chunk of d_gate (full gate), stored with one 16-byte write
+    float dgv[VEC];  // this chunk of d_gate (full gate), stored with 16-byte writes
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const float dov = Elem<T>::to_f(g[e]);
       dl = fmaf(Elem<T>::to_f(o[e]), dov, dl);
-      dgv[e] = Elem<T>::from_f(dov * oc[e]);
+      dgv[e] = dov * oc[e];
       if (outc) {
         dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[e]);
         if (gate_mode == 2) dg = fmaf(dov, oc[e], dg);
       }
     }
-    if (outc && (gate_mode == 1 || gate_mode == 3))
-      *reinterpret_cast<u32x4*>(d_gate + goff) = *reinterpret_cast<const u32x4*>(dgv);
+    if (outc && (gate_mode == 1 || gate_mode == 3)) store_gate<G, VEC>(d_gate + goff, dgv);
     // reduce over the tpr lanes of this row (contiguous lanes)
     for (int o2 = tpr >> 1; o2 > 0; o2 >>= 1) {
       dl += __shfl_xor(dl, o2, 64);
@@ -273,7 +298,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     }
     if (col == 0) {
       delta[tok] = dl;
-      if (outc && gate_mode == 2) d_gate[tok] = Elem<T>::from_f(dg);
+      if (outc && gate_mode == 2) d_gate[tok] = Elem<G>::from_f(dg);
     }
   }
   if (outc) {
@@ -285,6 +310,54 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       for (int r = 0; r < rpi; ++r) s += part[r * D + d];
       d_outc[blk * D + d] = Elem<T>::from_f(s);
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stand-alone combine for an fp32 gate beside T inputs (the fused epilogue of
+// the fine forward reads the gate in T):
+//   out[tok] = T(out_c[block] * gate[tok] + fine[tok]),
+// the reference's fused combine over its T-rounded sparse output
+// (fused_common.py:175-199).  out may alias fine.  One workgroup per
+// (bh, query block), 16-byte chunks.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void combine_f32gate_kernel(
+    const T* fine, const T* __restrict__ outc, const float* __restrict__ gate, int gate_mode,
+    int gate_heads, T* out, int qb, int D, int be) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t blk = blockIdx.x + (int64_t)blockIdx.y * qb;
+  const int tpr = D / VEC, rpi = 256 / tpr;
+  const int col = threadIdx.x % tpr, row0 = threadIdx.x / tpr;
+  const int c0 = col * VEC;
+  float oc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) oc[e] = Elem<T>::to_f(outc[blk * D + c0 + e]);
+  const int64_t bh = blockIdx.y;
+  const int64_t sq = (int64_t)qb * be;
+  const int64_t gbase = gate_mode == 3
+                            ? ((bh / gate_heads) * sq * gate_heads + bh % gate_heads) * D + c0
+                            : 0;
+  for (int t = row0; t < be; t += rpi) {
+    const int64_t tok = blk * be + t;
+    const int64_t off = tok * D + c0;
+    const int64_t goff = gate_mode == 3
+                             ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
+                             : off;
+    float gv[VEC];
+    if (gate_mode == 1 || gate_mode == 3) {
+      load_gate<float, VEC>(gate + goff, gv);
+    } else {
+      const float gs = gate_mode == 2 ? gate[tok] : 1.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) gv[e] = gs;
+    }
+    u32x4 rf = *reinterpret_cast<const u32x4*>(fine + off);
+    const T* f = reinterpret_cast<const T*>(&rf);
+    T o[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[e] = Elem<T>::from_f(fmaf(oc[e], gv[e], Elem<T>::to_f(f[e])));
+    *reinterpret_cast<u32x4*>(out + off) = *reinterpret_cast<const u32x4*>(o);
   }
 }
 
@@ -461,7 +534,9 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
                             float* delta, void* d_out_c, void* d_gate, int64_t bh, int64_t sq,
                             int32_t D, int32_t be, int32_t dtype, void* stream) {
   if (!fine_out || !dout || !delta) return VSA_ERR_NULL;
-  if (gate_mode < 0 || gate_mode > 3) return VSA_ERR_SHAPE;
+  const bool gate_f32 = (gate_mode & VSA_GATE_F32) != 0;
+  gate_mode &= ~VSA_GATE_F32;
+  if (gate_mode < 0 || gate_mode > 3 || (gate_f32 && gate_mode == 0)) return VSA_ERR_SHAPE;
   if (out_c && gate_mode == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
   if (out_c && !d_out_c) return VSA_ERR_NULL;
   if (out_c && gate_mode != 0 && (!gate || !d_gate)) return VSA_ERR_NULL;
@@ -470,12 +545,33 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
   const int qb = (int)(sq / be);
   hipStream_t s = (hipStream_t)stream;
   VSA_DISPATCH_ALL(dtype, T, {
-    hipLaunchKernelGGL(bwd_prep_kernel<T>, dim3(qb, (unsigned)bh), dim3(256), 0, s,
-                       (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate, gate_mode,
-                       gate_heads, delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
+    if (gate_f32)
+      hipLaunchKernelGGL((bwd_prep_kernel<T, float>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
+                         (const T*)fine_out, (const T*)dout, (const T*)out_c,
+                         (const float*)gate, gate_mode, gate_heads, delta, (T*)d_out_c,
+                         (float*)d_gate, qb, D, be);
+    else
+      hipLaunchKernelGGL((bwd_prep_kernel<T, T>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
+                         (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate,
+                         gate_mode, gate_heads, delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
   });
   return vsa_check_launch();
 }
+
+namespace vsa {
+int combine_f32gate(const void* fine, const void* out_c, const void* gate, int gate_mode,
+                    int gate_heads, void* out, int64_t bh, int64_t sq, int D, int be, int dtype,
+                    hipStream_t s) {
+  if (bh <= 0 || be <= 0 || sq <= 0 || sq % be || !vec_dim_ok(D, dtype)) return VSA_ERR_SHAPE;
+  const int qb = (int)(sq / be);
+  VSA_DISPATCH_ALL(dtype, T, {
+    hipLaunchKernelGGL((combine_f32gate_kernel<T>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
+                       (const T*)fine, (const T*)out_c, (const float*)gate, gate_mode,
+                       gate_heads, (T*)out, qb, D, be);
+  });
+  return vsa_check_launch();
+}
+}  // namespace vsa
 
 extern "C" int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c,
                               const float* probs, const void* d_out_c, float* ds, void* d_q_c,

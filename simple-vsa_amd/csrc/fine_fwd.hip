@@ -670,6 +670,20 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                               int32_t gate_heads, int64_t bh, int64_t sq, int64_t skv, int32_t D,
                               int32_t be, int32_t topk, float scale, int32_t dtype, void* stream) {
   if (!q || !k || !v || !selected || !kv_vbs || !out) return VSA_ERR_NULL;
+  if (out_c && (gate_mode & VSA_GATE_F32) && dtype != VSA_F32) {
+    // fp32 gate beside T inputs: fine output in T (into fine_out, or into out
+    // when no backward needs it), then the combine as a second pass
+    const int gm = gate_mode & ~VSA_GATE_F32;
+    if (gm < 1 || gm > 3 || !gate) return gm == 0 ? VSA_ERR_SHAPE : VSA_ERR_NULL;
+    if (gm == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
+    void* fine = fine_out ? fine_out : out;
+    int rc = vsa_sparse_fwd(q, k, v, selected, kv_vbs, fine, nullptr, lse, nullptr, nullptr, 0,
+                            gate_heads, bh, sq, skv, D, be, topk, scale, dtype, stream);
+    if (rc != VSA_OK) return rc;
+    return combine_f32gate(fine, out_c, gate, gm, gate_heads, out, bh, sq, D, be, dtype,
+                           (hipStream_t)stream);
+  }
+  gate_mode &= ~VSA_GATE_F32;  // an fp32 gate beside fp32 inputs is the plain case
   if (gate_mode < 0 || gate_mode > 3) return VSA_ERR_SHAPE;
   if (out_c && gate_mode == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
   if (out_c && gate_mode != 0 && !gate) return VSA_ERR_NULL;

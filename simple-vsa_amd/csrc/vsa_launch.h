@@ -55,3 +55,11 @@ static inline int cu_count() {
   }
   return cached[dev];
 }
+
+namespace vsa {
+// out = T(out_c[block] * gate + fine) with an fp32 gate (common.hip); out may
+// alias fine.  gate_mode is 1, 2 or 3 (without the VSA_GATE_F32 flag).
+int combine_f32gate(const void* fine, const void* out_c, const void* gate, int gate_mode,
+                    int gate_heads, void* out, int64_t bh, int64_t sq, int D, int be, int dtype,
+                    hipStream_t s);
+}  // namespace vsa

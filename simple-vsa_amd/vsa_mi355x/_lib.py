@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 GATE_NONE, GATE_FULL, GATE_PER_TOKEN, GATE_TOKEN_MAJOR = 0, 1, 2, 3
+GATE_F32 = 4   # flag: an fp32 gate beside bf16 / fp16 inputs
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

@@ -267,7 +267,7 @@ def sparse_forward(q, k, v, selected, variable_block_sizes, block_elements, scal
     out = torch.empty_like(q)
     lse = (torch.empty((b, h, sq), device=q.device, dtype=torch.float32) if want_lse else None)
     fine = torch.empty_like(q) if (want_lse and out_c is not None) else None
-    gmode = _gate_mode(gate, d) if out_c is not None else _lib.GATE_NONE
+    gmode = _gate_mode(gate, d, q.dtype) if out_c is not None else _lib.GATE_NONE
     _lib.call("vsa_sparse_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(selected),
               _lib.ptr(variable_block_sizes), _lib.ptr(out), _lib.ptr(fine), _lib.ptr(lse),
               _lib.ptr(out_c), _lib.ptr(gate if gmode else None), gmode, h, b * h, sq, skv, d,
@@ -285,12 +285,19 @@ def _token_major(gate: Tensor) -> bool:
     return gate.stride() == (s * h * d, d, h * d, 1) and not gate.is_contiguous()
 
 
-def _gate_mode(gate: Optional[Tensor], d: int) -> int:
+def _gate_mode(gate: Optional[Tensor], d: int, dtype: torch.dtype) -> int:
+    """C-ABI gate mode: layout, plus the fp32 flag for an fp32 gate beside
+    bf16 / fp16 inputs."""
     if gate is None:
         return _lib.GATE_NONE
     if gate.shape[-1] == 1 and d != 1:
-        return _lib.GATE_PER_TOKEN
-    return _lib.GATE_TOKEN_MAJOR if _token_major(gate) else _lib.GATE_FULL
+        mode = _lib.GATE_PER_TOKEN
+    else:
+        mode = _lib.GATE_TOKEN_MAJOR if _token_major(gate) else _lib.GATE_FULL
+    if gate.dtype != dtype:
+        assert gate.dtype == torch.float32, gate.dtype
+        mode |= _lib.GATE_F32
+    return mode
 
 
 def backward_prep(fine, dout, block_elements, *, out_c=None, gate=None):
@@ -300,9 +307,9 @@ def backward_prep(fine, dout, block_elements, *, out_c=None, gate=None):
     b, h, sq, d = out.shape
     delta = torch.empty((b, h, sq), device=out.device, dtype=torch.float32)
     d_outc = torch.empty_like(out_c) if out_c is not None else None
-    gmode = _gate_mode(gate, d) if out_c is not None else _lib.GATE_NONE
+    gmode = _gate_mode(gate, d, out.dtype) if out_c is not None else _lib.GATE_NONE
     d_gate = None
-    if gmode == _lib.GATE_TOKEN_MAJOR:   # gradient in the gate's own token-major layout
+    if (gmode & ~_lib.GATE_F32) == _lib.GATE_TOKEN_MAJOR:   # the gate's own token-major layout
         d_gate = torch.empty((b, sq, h, d), device=gate.device, dtype=gate.dtype).transpose(1, 2)
     elif gmode:
         d_gate = torch.empty_like(gate, memory_format=torch.contiguous_format)
@@ -468,13 +475,32 @@ class _VSA(torch.autograd.Function):
 
 
 def _prepare_gate(gate: Optional[Tensor], q: Tensor) -> Optional[Tensor]:
+    """The gate as the kernels read it, by differentiable torch ops (autograd
+    takes the gradient back to the caller's shape and dtype).
+
+    torch_vsa multiplies by ``compress_attn_weight.float()`` with broadcasting
+    (torch_impl.py:108-113), so any gate that broadcasts to q's shape is
+    accepted: one that varies along the head dim is expanded to [B, H, S, D],
+    one that does not to [B, H, S, 1].  A gate of q's dtype and of one of those
+    shapes is read as it is; any other is promoted with ``.float()`` first, as
+    the reference does, so its gradient is reduced over the broadcast dims in
+    fp32, and read as fp32 (the combine then runs as its own pass over the
+    T-rounded fine output, as the reference's fused combine does)."""
     if gate is None:
         return None
     b, h, s, d = q.shape
-    if tuple(gate.shape) not in ((b, h, s, d), (b, h, s, 1)):
-        raise ValueError(
-            "compress_attn_weight must have the same shape as q, or [batch, heads, seq_len, 1]")
-    gate = gate.to(device=q.device, dtype=q.dtype)
+    try:
+        ok = torch.broadcast_shapes(gate.shape, q.shape) == q.shape
+    except RuntimeError:
+        ok = False
+    if not ok:
+        raise ValueError("compress_attn_weight must have the same shape as q, or a shape that "
+                         "broadcasts to it (e.g. [batch, heads, seq_len, 1])")
+    gate = gate.to(device=q.device)
+    per_token = (gate.ndim == 0 or gate.shape[-1] == 1) and d != 1
+    full = (b, h, s, 1) if per_token else (b, h, s, d)
+    if gate.dtype != q.dtype or tuple(gate.shape) != full:
+        gate = gate.float().expand(full)
     # the gate producer's per-head view of its [B, S, H, D] output is consumed in place
     return gate if _token_major(gate) else gate.contiguous()
 

@@ -83,3 +83,78 @@ def test_gate_producer_trains_end_to_end_against_oracle():
     rw = layer.to_gate_compress.weight.grad
     rel = ((gw.float().cpu() - rw).norm() / rw.norm()).item()
     assert rel < 3e-2, rel
+
+
+# ---------------------------------------------------------------------------
+# Gates of another dtype or shape: torch_vsa multiplies by
+# compress_attn_weight.float() with broadcasting (torch_impl.py:108-113)
+# ---------------------------------------------------------------------------
+
+def _gate_case(gate_shape, gate_dtype, seed, tm=False, be=256, nb=4, h=3, d=128):
+    from vsa_mi355x import mi355x as M
+    g = torch.Generator().manual_seed(seed)
+    shape = (1, h, nb * be, d)
+    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
+    gate = torch.rand(gate_shape, generator=g).to(gate_dtype)
+    if tm:   # the producer's token-major layout, in fp32
+        gate = gate.transpose(1, 2).contiguous().transpose(1, 2)
+    vbs = torch.full((nb,), be)
+    vbs[1] = be - 19
+    leaves = [x.to(DEV).requires_grad_() for x in (q, k, v)]
+    gd = gate.to(DEV)
+    if tm:
+        gd = gd.transpose(1, 2).contiguous().transpose(1, 2)
+    gd.requires_grad_()
+    out = M.mi355x_vsa(*leaves, vbs.to(DEV), vbs.to(DEV), 2, (1, 1, be), gd)
+    grads = torch.autograd.grad(out, leaves + [gd], do.to(DEV))
+    _, sel = M.mi355x_route(*(x.detach() for x in leaves), vbs.to(DEV), vbs.to(DEV), 2,
+                            (1, 1, be))
+    ref_leaves = [x.clone().requires_grad_() for x in (q, k, v, gate)]
+    ref = O.torch_vsa(*ref_leaves[:3], vbs, vbs, 2, (1, 1, be), ref_leaves[3],
+                      selected=sel.cpu().long())
+    ref_grads = torch.autograd.grad(ref, ref_leaves, do)
+    assert grads[3].dtype == gate_dtype and grads[3].shape == gate.shape
+    for name, a, e in zip(("out", "dq", "dk", "dv", "dgate"), [out] + list(grads),
+                          [ref] + list(ref_grads)):
+        a, e = a.detach().float().cpu(), e.detach().float().cpu()
+        diff = (a - e).abs().max().item()
+        rel = ((a - e).norm() / e.norm()).item()
+        assert diff <= 2e-2 and rel <= 1e-2, f"{name}: max-abs {diff:.3e}, rel-L2 {rel:.3e}"
+    return gd, grads
+
+
+@pytest.mark.parametrize("kind", ["full", "token", "token_major"])
+def test_fp32_gate_beside_bf16_inputs(kind):
+    """The gate stays fp32 (the reference promotes it, it does not round it to
+    bf16) and its gradient comes back in fp32."""
+    shape = (1, 3, 1024, 1) if kind == "token" else (1, 3, 1024, 128)
+    _gate_case(shape, torch.float32, 81, tm=kind == "token_major")
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1024, 1), (1, 3, 1, 128), (1024, 128), (128,),
+                                   (1, 3, 1024, 1)])
+def test_broadcast_gate_shapes(shape):
+    """Any gate shape that broadcasts to [B, H, S, D]; the gradient is reduced
+    back to the gate's own shape."""
+    _gate_case(shape, torch.bfloat16, 83)
+
+
+def test_fp32_gate_no_grad_forward_equals_grad_forward():
+    from vsa_mi355x import mi355x as M
+    g = torch.Generator(device=DEV).manual_seed(85)
+    q, k, v = (torch.randn(1, 2, 1024, 128, generator=g, device=DEV, dtype=torch.bfloat16)
+               for _ in range(3))
+    gate = torch.rand(1, 2, 1024, 128, generator=g, device=DEV, dtype=torch.float32)
+    vbs = torch.full((4,), 256, device=DEV, dtype=torch.int32)
+    with torch.no_grad():
+        a = M.mi355x_vsa(q, k, v, vbs, vbs, 2, (4, 8, 8), gate)
+    b = M.mi355x_vsa(q.requires_grad_(), k, v, vbs, vbs, 2, (4, 8, 8), gate)
+    assert torch.equal(a, b.detach())
+
+
+def test_gate_that_does_not_broadcast_is_rejected():
+    from vsa_mi355x import mi355x as M
+    q = torch.randn(1, 2, 512, 64, device=DEV, dtype=torch.bfloat16)
+    vbs = torch.full((2,), 256, device=DEV, dtype=torch.int32)
+    with pytest.raises(ValueError, match="compress_attn_weight"):
+        M.mi355x_vsa(q, q, q, vbs, vbs, 1, (4, 8, 8), torch.rand(1, 2, 512, 32, device=DEV))
