@@ -244,8 +244,8 @@ __device__ __forceinline__ X opaque(X x) {
 // x / c for an integer-valued c >= 1, correctly rounded, given r = RN(1/c):
 // q = x * r is within an ulp of x / c, and one FMA residual step rounds it
 // correctly (Markstein's theorem) -- three operations instead of a full
-// division.  Bit-identical to the division for every finite bf16 x and every
-// c in [1, 1024] (checked exhaustively on the host).
+// division.  Bit-identical to the division for every finite bf16 x, every
+// finite fp16 x and every c in [1, 1024] (checked exhaustively on the host).
 __device__ __forceinline__ float div_by_count(float x, float c, float r) {
   const float q0 = x * r;
   return fmaf(fmaf(-q0, c, x), r, q0);
