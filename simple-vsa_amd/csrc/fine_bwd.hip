@@ -729,8 +729,8 @@ __device__ __forceinline__ void dq_pp_tile(
     if (pvalid) {
       const int64_t off = ((int64_t)pkv * BE + pc * C::KC) * D;
       T* Ks = smem + stg * C::STAGE;
-      tdma.copy(Ks, kbase + off);
-      tdma.copy(Ks + C::TILE, vbase + off);
+      tdma.copy(Ks, kbase + off, wave);
+      tdma.copy(Ks + C::TILE, vbase + off, wave);
       nv = min(pnvb - pc * C::KC, C::KC);
       ++pc;
       pvalid = route.next(ps, pc, pkv, pnvb);
@@ -781,6 +781,20 @@ __device__ __forceinline__ void dq_pp_tile(
   // MFMAs ahead of its use (head_dim 128: 2, the most that does not spill
   // inside the chunk loop).
   constexpr int NSP = 4 * (D / 16), NDQ = 4 * (D / 32), L = D == 128 ? 2 : 8;
+  // Deeper stream while the dQ products run: the S / dP accumulators are not
+  // live yet, so their registers hold operands instead.
+  constexpr int LD = 8;
+  // The first L operands of a phase with the dQ products (K^T pieces of chunk
+  // j-1, in LDS since long before) are read at the end of the preceding VALU
+  // phase, so the MFMA phase does not open with an LDS round trip.
+  static_assert(L <= NDQ, "the prefetched operands are K^T pieces");
+  V8 pre[L];
+  auto prefetch = [&](int sp) {
+    const char* Kp = smem_c + sp * C::STAGE * (int)sizeof(T);
+    __builtin_amdgcn_sched_barrier(0);  // after the VALU phase's arithmetic
+#pragma unroll
+    for (int u = 0; u < L; ++u) pre[u] = t_tr(Kp, u % (D / 32), u / (D / 32));
+  };
   auto mma_x = [&](int sj, int sp, auto with_dq) {
     constexpr int N0 = decltype(with_dq)::value ? NDQ : 0;  // dQ products first
     constexpr int NX = N0 + NSP;
@@ -800,12 +814,27 @@ __device__ __forceinline__ void dq_pp_tile(
       }
     };
 #pragma unroll
-    for (int smt = 0; smt < 2; ++smt) sacc[smt] = pacc[smt] = f32x16{};
-#pragma unroll
-    for (int u = 0; u < L; ++u) load(u);
+    for (int u = 0; u < L; ++u) {
+      if (N0 > 0)
+        op[u] = pre[u];
+      else
+        load(u);
+    }
+    // last operand index loaded by the time MFMA u issues: u + LD during the
+    // dQ products, u + L after them (never less than already loaded)
+    auto hi = [](int u) {
+      if (u < 0) return L - 1;
+      if (u < N0) return u + LD;
+      return (N0 > 0 && N0 - 1 + LD > u + L) ? N0 - 1 + LD : u + L;
+    };
 #pragma unroll
     for (int u = 0; u < NX; ++u) {
-      load(u + L);
+#pragma unroll
+      for (int x = hi(u - 1) + 1; x <= hi(u); ++x) load(x);
+      if (u == N0) {
+#pragma unroll
+        for (int smt = 0; smt < 2; ++smt) sacc[smt] = pacc[smt] = f32x16{};
+      }
       if (u < N0) {
         dqacc[u % (D / 32)] = E::mfma32(op[u], bs[u / (D / 32)], dqacc[u % (D / 32)]);
       } else {
@@ -868,19 +897,23 @@ __device__ __forceinline__ void dq_pp_tile(
     dma_wait();  // this wave's copies of chunk 1
     phase_barrier();
     int nv2 = issue(2);
-    valu(nv0);
+    int fin = nv0;  // valid keys of the chunk whose VALU phase is pending
     nvm1 = nv0;
     nv0 = nv1;
     nv1 = nv2;
     // chunks 1 .. n; at j = n (no chunk j) S and dP run on a stage no copy is
-    // writing and their results are not used
+    // writing and their results are not used.  An iteration opens with the
+    // VALU phase of chunk j-1, so the operands prefetched at its end stay
+    // inside one iteration.
     for (int j = 1; nvm1 > 0; ++j) {
+      if (fin > 0) valu(fin);
+      prefetch((j - 1) % C::NS);
       phase_barrier();
       mma_x(j % C::NS, (j - 1) % C::NS, WithDq{});
       dma_wait();  // this wave's copies of chunk j+1
       phase_barrier();
       nv2 = issue((j + 2) % C::NS);
-      if (nv0 > 0) valu(nv0);
+      fin = nv0;
       nvm1 = nv0;
       nv0 = nv1;
       nv1 = nv2;

@@ -345,8 +345,8 @@ __device__ __forceinline__ void fwd_pp_tile(
     if (pvalid) {
       const int64_t off = ((int64_t)pkv * BE + pc * C::KC) * D;
       T* Ks = smem + stg * C::STAGE;
-      tdma.copy(Ks, kbase + off);
-      tdma.copy(Ks + C::TILE, vbase + off);
+      tdma.copy(Ks, kbase + off, wave);
+      tdma.copy(Ks + C::TILE, vbase + off, wave);
       nv = min(pnvb - pc * C::KC, C::KC);
       ++pc;
       pvalid = route.next(ps, pc, pkv, pnvb);
@@ -489,6 +489,18 @@ __device__ __forceinline__ void fwd_pp_tile(
   // L is as deep as the registers allow without spills inside the chunk loop
   // (head_dim 128: 6, 2 % faster than 4; 7 spills there).
   constexpr int NSX = 2 * (D / 16), NOX = 4 * (D / 32), NX = NSX + NOX, L = D == 128 ? 6 : 8;
+  // The first L operands of an MFMA phase (K rows of its chunk, published by
+  // the barrier that opens the previous softmax phase) are read at the end of
+  // that softmax phase, so the phase does not open with an LDS round trip.
+  constexpr int NP = L;  // prefetched operands
+  V8 pre[NP];
+  auto prefetch = [&](int sj) {
+    const char* Kb = smem_c + sj * C::STAGE * (int)sizeof(T);
+    __builtin_amdgcn_sched_barrier(0);  // after the softmax phase's arithmetic
+#pragma unroll
+    for (int u = 0; u < NP; ++u) pre[u] = k_row(Kb, u >> 1, u & 1);
+  };
+  static_assert(L <= NSX, "the prefetched operands are K rows");
   auto mma_so = [&](int sj, int sp, int nv) {
     const char* Kb = smem_c + sj * C::STAGE * (int)sizeof(T);
     const char* Vb = smem_c + (sp * C::STAGE + C::TILE) * (int)sizeof(T);
@@ -505,7 +517,12 @@ __device__ __forceinline__ void fwd_pp_tile(
     sacc[0] = f32x16{};
     sacc[1] = f32x16{};
 #pragma unroll
-    for (int u = 0; u < L; ++u) load(u);
+    for (int u = 0; u < L; ++u) {
+      if (u < NP)
+        op[u] = pre[u];
+      else
+        load(u);
+    }
 #pragma unroll
     for (int u = 0; u < NX; ++u) {
       load(u + L);
@@ -547,7 +564,12 @@ __device__ __forceinline__ void fwd_pp_tile(
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
-  if (grp1) phase_barrier();
+  if (grp1) {
+    phase_barrier();
+    // group 1's copies of chunk 1 land before the barrier after which group 0
+    // reads chunk 1 (its operand prefetch opens its next softmax phase)
+    dma_wait();
+  }
   if (nv0 > 0) {
     // chunk 0: no chunk -1, so its MFMA phase is S_0 alone
     phase_barrier();
@@ -556,22 +578,31 @@ __device__ __forceinline__ void fwd_pp_tile(
     dma_wait();  // this wave's copies of chunk 1
     phase_barrier();
     int nv2 = issue(2);
-    finish(nv0);
+    int fin = nv0;  // valid keys of the chunk whose softmax phase is pending
     nvm1 = nv0;
     nv0 = nv1;
     nv1 = nv2;
     // chunks 1 .. n; at j = n (no chunk j) the S half of the stream runs on a
-    // stage no copy is writing and its result is not used
+    // stage no copy is writing and its result is not used.  An iteration opens
+    // with the softmax phase of chunk j-1, so the operands prefetched at its
+    // end stay inside one iteration.  Chunk j+1 is complete in LDS at the
+    // barrier that ends group 0's MFMA phase of chunk j (and opens group 1's):
+    // group 0 waits for its copies of it before that barrier, group 1, whose
+    // copies were issued at the start of the softmax phase just ending, at the
+    // end of that phase.  Group 0 prefetches from chunk j+1 right after it.
     for (int j = 1; nvm1 > 0; ++j) {
+      if (fin > 0) finish(fin);
+      if (grp1) dma_wait();  // this wave's copies of chunk j+1
+      prefetch(j % C::NS);
       phase_barrier();
       mma_so(j % C::NS, (j - 1) % C::NS, nv0);
-      dma_wait();  // this wave's copies of chunk j+1
+      if (!grp1) dma_wait();  // this wave's copies of chunk j+1
       phase_barrier();
       // the stage of chunk j+2 last held chunk j-2, read for the last time in
       // group 1's MFMA phase of chunk j-1, which ended before this iteration's
       // first barrier
       nv2 = issue((j + 2) % C::NS);
-      if (nv0 > 0) finish(nv0);
+      fin = nv0;
       nvm1 = nv0;
       nv0 = nv1;
       nv1 = nv2;

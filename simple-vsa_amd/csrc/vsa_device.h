@@ -312,6 +312,13 @@ struct TileDma {
 #pragma unroll
     for (int i = 0; i < N; ++i) dma16_s(voff[i], src, base + (uint32_t)i * (NT / 64) * 1024u);
   }
+  // copy() with the caller's wave index held in a scalar register (no vector
+  // temporary of the thread index stays live across the caller's loop)
+  __device__ __forceinline__ void copy(T* dst, const T* src, int wave) const {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst)) + (uint32_t)wave * 1024u;
+#pragma unroll
+    for (int i = 0; i < N; ++i) dma16_s(voff[i], src, base + (uint32_t)i * (NT / 64) * 1024u);
+  }
 };
 
 // Wait until at most N of this wave's vector-memory loads are outstanding.
