@@ -44,7 +44,23 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(
   float acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-  for (int t = row0; t < valid; t += rpi) {
+  // eight rows' loads in flight per thread before their sums (a load per
+  // iteration leaves too few bytes in flight to cover HBM latency)
+  constexpr int UR = 8;
+  int t = row0;
+  for (; t + (UR - 1) * rpi < valid; t += UR * rpi) {
+    u32x4 raw[UR];
+#pragma unroll
+    for (int u = 0; u < UR; ++u)
+      raw[u] = *reinterpret_cast<const u32x4*>(base + (int64_t)(t + u * rpi) * D + col * VEC);
+#pragma unroll
+    for (int u = 0; u < UR; ++u) {
+      const T* vals = reinterpret_cast<const T*>(&raw[u]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] += Elem<T>::to_f(vals[e]);
+    }
+  }
+  for (; t < valid; t += rpi) {
     u32x4 raw = *reinterpret_cast<const u32x4*>(base + (int64_t)t * D + col * VEC);
     const T* vals = reinterpret_cast<const T*>(&raw);
 #pragma unroll
@@ -258,47 +274,77 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
   const int64_t gbase = gate_mode == 3
                             ? ((bh / gate_heads) * sq * gate_heads + bh % gate_heads) * D + c0
                             : 0;
-#pragma unroll 4
-  for (int t = row0; t < be; t += rpi) {
-    const int64_t tok = blk * be + t;
-    const int64_t off = tok * D + c0;
-    // offset of this token's gate (and d_gate) chunk
-    const int64_t goff = gate_mode == 3
-                             ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
-                             : off;
-    u32x4 ro = *reinterpret_cast<const u32x4*>(fine + off);
-    u32x4 rd = *reinterpret_cast<const u32x4*>(dout + off);
-    const T* o = reinterpret_cast<const T*>(&ro);
-    const T* g = reinterpret_cast<const T*>(&rd);
-    float gv[VEC];
-    if (gate_mode == 1 || gate_mode == 3) {
-      load_gate<G, VEC>(gate + goff, gv);
-    } else {
-      const float gs = gate_mode == 2 ? Elem<G>::to_f(gate[tok]) : 1.f;
+  // UR rows per pass: their loads are issued together and their row
+  // reductions run as UR independent chains (one row per pass left a single
+  // load and a serial shuffle chain per iteration)
+  constexpr int UR = 4;
+  for (int t0 = row0; t0 < be; t0 += UR * rpi) {
+    u32x4 ro[UR], rd[UR];
+    float gv[UR][VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) gv[e] = gs;
-    }
-    float dl = 0.f, dg = 0.f;
-    float dgv[VEC];  // this chunk of d_gate (full gate), stored with 16-byte writes
+    for (int u = 0; u < UR; ++u) {
+      const int t = t0 + u * rpi;
+      if (t >= be) break;
+      const int64_t tok = blk * be + t;
+      const int64_t off = tok * D + c0;
+      ro[u] = *reinterpret_cast<const u32x4*>(fine + off);
+      rd[u] = *reinterpret_cast<const u32x4*>(dout + off);
+      if (gate_mode == 1 || gate_mode == 3) {
+        // offset of this token's gate (and d_gate) chunk
+        const int64_t goff = gate_mode == 3
+                                 ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
+                                 : off;
+        load_gate<G, VEC>(gate + goff, gv[u]);
+      } else {
+        const float gs = gate_mode == 2 ? Elem<G>::to_f(gate[tok]) : 1.f;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float dov = Elem<T>::to_f(g[e]);
-      dl = fmaf(Elem<T>::to_f(o[e]), dov, dl);
-      dgv[e] = dov * oc[e];
-      if (outc) {
-        dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[e]);
-        if (gate_mode == 2) dg = fmaf(dov, oc[e], dg);
+        for (int e = 0; e < VEC; ++e) gv[u][e] = gs;
       }
     }
-    if (outc && (gate_mode == 1 || gate_mode == 3)) store_gate<G, VEC>(d_gate + goff, dgv);
-    // reduce over the tpr lanes of this row (contiguous lanes)
+    float dl[UR], dg[UR];
+#pragma unroll
+    for (int u = 0; u < UR; ++u) dl[u] = dg[u] = 0.f;
+#pragma unroll
+    for (int u = 0; u < UR; ++u) {
+      const int t = t0 + u * rpi;
+      if (t >= be) break;
+      const T* o = reinterpret_cast<const T*>(&ro[u]);
+      const T* g = reinterpret_cast<const T*>(&rd[u]);
+      float dgv[VEC];  // this chunk of d_gate (full gate), stored with 16-byte writes
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float dov = Elem<T>::to_f(g[e]);
+        dl[u] = fmaf(Elem<T>::to_f(o[e]), dov, dl[u]);
+        dgv[e] = dov * oc[e];
+        if (outc) {
+          dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[u][e]);
+          if (gate_mode == 2) dg[u] = fmaf(dov, oc[e], dg[u]);
+        }
+      }
+      if (outc && (gate_mode == 1 || gate_mode == 3)) {
+        const int64_t goff = gate_mode == 3
+                                 ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
+                                 : (blk * be + t) * D + c0;
+        store_gate<G, VEC>(d_gate + goff, dgv);
+      }
+    }
+    // reduce over the tpr lanes of each row (contiguous lanes)
     for (int o2 = tpr >> 1; o2 > 0; o2 >>= 1) {
-      dl += __shfl_xor(dl, o2, 64);
-      dg += __shfl_xor(dg, o2, 64);
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        dl[u] += __shfl_xor(dl[u], o2, 64);
+        dg[u] += __shfl_xor(dg[u], o2, 64);
+      }
     }
     if (col == 0) {
-      delta[tok] = dl;
-      if (outc && gate_mode == 2) d_gate[tok] = Elem<G>::from_f(dg);
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        const int t = t0 + u * rpi;
+        if (t >= be) break;
+        const int64_t tok = blk * be + t;
+        delta[tok] = dl[u];
+        if (outc && gate_mode == 2) d_gate[tok] = Elem<G>::from_f(dg[u]);
+      }
     }
   }
   if (outc) {
