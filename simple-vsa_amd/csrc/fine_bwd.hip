@@ -503,10 +503,6 @@ __device__ __forceinline__ void dkdv_tile(
       V8 bp[2], bs[2];
       bp[0] = pack8<T>(pv);
       bs[0] = pack8<T>(dsv);
-      // descriptor of the copy issued by the next step (its CSR entry is an
-      // LDS read; doing it here keeps it off the next step's critical path)
-      const int nn = it + NS;
-      cpn = copy_of(nn < items ? nn : items - 1);
 #pragma unroll
       for (int vv = 0; vv < NC; ++vv) {
         issue(NA + vv + L);
@@ -524,6 +520,13 @@ __device__ __forceinline__ void dkdv_tile(
       }
 #pragma unroll
       for (int x = NA + NC + L; x < NA + NC + 4; ++x) issue(x);
+      // descriptor of the copy issued by the next step (its CSR entry is an
+      // LDS read, kept off the next step's critical path).  It comes after
+      // both MFMA phases: the CSR refill branch inside it splits the code, and
+      // placed between the phases it let the compiler sink B(i) (used only by
+      // C(i)) past the branch, out from under the MFMAs of A(i+1).
+      const int nn = it + NS;
+      cpn = copy_of(nn < items ? nn : items - 1);
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
