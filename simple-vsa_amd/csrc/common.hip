@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(
     u32x4 raw[UR];
 #pragma unroll
     for (int u = 0; u < UR; ++u)
-      raw[u] = *reinterpret_cast<const u32x4*>(base + (int64_t)(t + u * rpi) * D + col * VEC);
+      raw[u] = ld_stream(reinterpret_cast<const u32x4*>(base + (int64_t)(t + u * rpi) * D + col * VEC));
 #pragma unroll
     for (int u = 0; u < UR; ++u) {
       const T* vals = reinterpret_cast<const T*>(&raw[u]);
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(
     }
   }
   for (; t < valid; t += rpi) {
-    u32x4 raw = *reinterpret_cast<const u32x4*>(base + (int64_t)t * D + col * VEC);
+    u32x4 raw = ld_stream(reinterpret_cast<const u32x4*>(base + (int64_t)t * D + col * VEC));
     const T* vals = reinterpret_cast<const T*>(&raw);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] += Elem<T>::to_f(vals[e]);
@@ -287,8 +287,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       if (t >= be) break;
       const int64_t tok = blk * be + t;
       const int64_t off = tok * D + c0;
-      ro[u] = *reinterpret_cast<const u32x4*>(fine + off);
-      rd[u] = *reinterpret_cast<const u32x4*>(dout + off);
+      ro[u] = ld_stream(reinterpret_cast<const u32x4*>(fine + off));
+      rd[u] = ld_stream(reinterpret_cast<const u32x4*>(dout + off));
       if (gate_mode == 1 || gate_mode == 3) {
         // offset of this token's gate (and d_gate) chunk
         const int64_t goff = gate_mode == 3
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(256) void combine_f32gate_kernel(
 #pragma unroll
       for (int e = 0; e < VEC; ++e) gv[e] = gs;
     }
-    u32x4 rf = *reinterpret_cast<const u32x4*>(fine + off);
+    u32x4 rf = ld_stream(reinterpret_cast<const u32x4*>(fine + off));
     const T* f = reinterpret_cast<const T*>(&rf);
     T o[VEC];
 #pragma unroll

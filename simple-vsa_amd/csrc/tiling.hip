@@ -19,6 +19,7 @@
 #include <stdint.h>
 
 #include "../../include/vsa_capi.h"
+#include "vsa_device.h"
 #include "vsa_launch.h"
 
 namespace vsa {
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(256) void rows_move_kernel(
   for (int64_t b = blockIdx.y; b < batch; b += gridDim.y) {
     const V* sp = reinterpret_cast<const V*>(x + (b * x_rows + s) * xc * VB);
     V* dp = reinterpret_cast<V*>(out + (b * out_rows + d) * oc * VB);
-    for (int64_t c = lane; c < oc; c += tpr) dp[c] = c < cc ? sp[c] : V{};
+    for (int64_t c = lane; c < oc; c += tpr) st_stream(dp + c, c < cc ? ld_stream(sp + c) : V{});
   }
 }
 
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(256) void rows_zero_kernel(char* __restrict__ out, 
   const int lane = threadIdx.x & (tpr - 1);
   for (int64_t b = blockIdx.y; b < batch; b += gridDim.y) {
     V* dp = reinterpret_cast<V*>(out + (b * out_rows + j) * cpr * VB);
-    for (int64_t c = lane; c < cpr; c += tpr) dp[c] = V{};
+    for (int64_t c = lane; c < cpr; c += tpr) st_stream(dp + c, V{});
   }
 }
 

@@ -81,6 +81,20 @@ __device__ __forceinline__ typename Elem<T>::vec8 as_vec8(u32x4 x) {
   return __builtin_bit_cast(typename Elem<T>::vec8, x);
 }
 
+// Streaming global accesses for data a pass touches once: non-temporal loads
+// of the token rows in the block means, the backward preprocessing and the
+// fp32-gate combine, loads and 16-byte stores of the row moves (8-12 % faster
+// there).  The fine kernels' 8-byte epilogue stores and the gate's loads and
+// stores measured slower with them (up to 8 %), so those stay plain.
+template <typename V>
+__device__ __forceinline__ V ld_stream(const V* p) {
+  return __builtin_nontemporal_load(p);
+}
+template <typename V>
+__device__ __forceinline__ void st_stream(V* p, V v) {
+  __builtin_nontemporal_store(v, p);
+}
+
 // Total-order integer key of a score: larger score -> larger key; -0 == +0;
 // NaN above +inf (torch.topk's ranking).
 __device__ __forceinline__ int order_key(float x) {
