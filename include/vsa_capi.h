@@ -287,6 +287,94 @@ int vsa_rows_zero_unmarked(void* out, int64_t out_rows, int64_t batch, int64_t r
                            const int64_t* marked, int64_t n_marked, uint8_t* mark_workspace,
                            void* stream);
 
+/*
+ * ---- Tiled sequences: tile() / untile() fused into the op -------------------
+ *
+ * The reference tiles a raster-order video sequence before the op and untiles
+ * the output after it as separate passes (tile: fastvideo_tiling.py:130-140,
+ * untile: 143-145).  The entry points below run the op on raster-order
+ * q, k, v, gate and dout and return raster-order out, dq, dk, dv and d_gate
+ * directly: the passes that read the data anyway (block mean, backward
+ * preprocessing) also write the tiled copies the fine kernels consume, and
+ * the fine kernels' epilogues store their results at raster rows.  Every
+ * value equals the unfused composition tile -> op -> untile bit for bit.
+ * slot_rows[nb*be] (int32) maps a tiled slot n*be + p to its raster token,
+ * -1 for a padding slot; it is shared by every batch and head.  s_out is the
+ * raster length T*H*W, sq = skv = nb*be the tiled length.  bf16 / fp16, head
+ * dims 64 and 128, tiles of 64, 128 or 256 tokens; gate_mode 0, 1 or 2 in the
+ * input dtype (callers fall back to the composition otherwise).
+ */
+
+/*
+ * slot_rows for a (T, H, W) latent in (ts, hs, ws) tiles (ceil(T/ts) *
+ * ceil(H/hs) * ceil(W/ws) * ts*hs*ws entries), from the closed form of the
+ * layout build_vsa_metadata describes (fastvideo_tiling.py:22-88): the
+ * inverse of tile_partition_indices / non_pad_index.
+ */
+int vsa_tile_slot_rows(int32_t T, int32_t H, int32_t W, int32_t ts, int32_t hs, int32_t ws,
+                       int32_t* slot_rows, void* stream);
+
+/*
+ * tile() of q, k, v [bh, s_out, D] into q_t, k_t, v_t [bh, nb*be, D] (zero rows
+ * at padding slots) and the padded block mean of the tiled copies into
+ * q_c, k_c, v_c [bh, nb, D], in one pass: vsa_pool_qkv after tile()
+ * (fused_block_mean, fused_common.py:20-59, on tile's output).
+ */
+int vsa_tile_pool_qkv(const void* q, const void* k, const void* v, const int32_t* slot_rows,
+                      const int32_t* variable_block_sizes, void* q_t, void* k_t, void* v_t,
+                      void* q_c, void* k_c, void* v_c, int64_t bh, int64_t s_out, int32_t nb,
+                      int32_t head_dim, int32_t block_elements, int32_t dtype, void* stream);
+
+/*
+ * vsa_sparse_fwd on tiled q, k, v with out (and a gate_mode 1 / 2 gate) in
+ * raster order [bh, s_out, ...]; fine_out and lse stay tiled.  Padding slots
+ * produce no out row.
+ */
+int vsa_sparse_fwd_tiled(const void* q, const void* k, const void* v, const int32_t* selected,
+                         const int32_t* kv_variable_block_sizes, void* out, void* fine_out,
+                         float* lse, const void* out_c, const void* gate, int32_t gate_mode,
+                         const int32_t* slot_rows, int64_t s_out, int64_t bh, int64_t sq,
+                         int64_t skv, int32_t head_dim, int32_t block_elements, int32_t topk,
+                         float scale, int32_t dtype, void* stream);
+
+/*
+ * vsa_bwd_prep with dout and the gate in raster order and d_gate written in
+ * raster order; fine_out, delta tiled.  Also writes dout_t [bh, sq, D], dout in
+ * the tiled layout with zero rows at padding slots (untile's gradient,
+ * fastvideo_tiling.py:143-145), for vsa_sparse_bwd_dq_tiled / _dkdv_tiled.
+ */
+int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const void* out_c,
+                       const void* gate, int32_t gate_mode, const int32_t* slot_rows,
+                       int64_t s_out, float* delta, void* d_out_c, void* d_gate, void* dout_t,
+                       int64_t bh, int64_t sq, int32_t head_dim, int32_t block_elements,
+                       int32_t dtype, void* stream);
+
+/*
+ * vsa_sparse_bwd_dq on tiled inputs (dout = dout_t) with dq written in raster
+ * order [bh, s_out, D]: tile()'s gradient (fastvideo_tiling.py:130-140) fused
+ * into the dQ epilogue.
+ */
+int vsa_sparse_bwd_dq_tiled(const void* q, const void* k, const void* v, const void* dout,
+                            const float* lse, const float* delta, const int32_t* selected,
+                            const int32_t* kv_variable_block_sizes, void* dq, const void* d_q_c,
+                            const int32_t* q_variable_block_sizes, const int32_t* slot_rows,
+                            int64_t s_out, int64_t bh, int64_t sq, int64_t skv,
+                            int32_t head_dim, int32_t block_elements, int32_t topk, float scale,
+                            int32_t dtype, void* stream);
+
+/*
+ * vsa_sparse_bwd_dkdv on tiled inputs with dk, dv written in raster order
+ * [bh, s_out, D] (tile()'s gradient fused into the dK/dV epilogue).
+ */
+int vsa_sparse_bwd_dkdv_tiled(const void* q, const void* k, const void* v, const void* dout,
+                              const float* lse, const float* delta, const int32_t* counts,
+                              const int32_t* offsets, const int32_t* inverse,
+                              const int32_t* kv_variable_block_sizes, void* dk, void* dv,
+                              const void* d_k_c, const void* d_v_c, const int32_t* slot_rows,
+                              int64_t s_out, int64_t bh, int64_t sq, int64_t skv,
+                              int32_t head_dim, int32_t block_elements, int32_t topk, float scale,
+                              int32_t* tile_order, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,80 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// tile() and the padded block mean in one pass: x (q, k or v) is a
+// raster-order sequence of s_out tokens per head; the tiled copy xt gets row
+// t of block n from raster row rows[n*be + t] (zero at a padding slot, < 0),
+// and the block mean sums the valid rows of that copy in the order
+// pool_qkv_kernel does, so both equal tile() followed by the pooling pass.
+// One workgroup per (tensor, bh, block).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void tile_pool_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ rows, const int32_t* __restrict__ vbs, T* __restrict__ qt,
+    T* __restrict__ kt, T* __restrict__ vt, T* __restrict__ qc, T* __restrict__ kc,
+    T* __restrict__ vc, int64_t bh, int nb, int D, int be, int64_t s_out) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float part[256 * VEC];
+  int64_t id = blockIdx.x;
+  const int64_t per = bh * nb;
+  const T* x = q;
+  T* xt = qt;
+  T* out = qc;
+  if (id >= 2 * per) {
+    id -= 2 * per; x = v; xt = vt; out = vc;
+  } else if (id >= per) {
+    id -= per; x = k; xt = kt; out = kc;
+  }
+  const int n = (int)(id % nb);
+  const int64_t head = id / nb;
+  const int32_t cnt = vbs[n];
+  const int valid = clamp_valid(cnt, be);
+  const float div = (float)(cnt > 1 ? cnt : 1);
+  const T* src = x + head * s_out * D;
+  T* dst = xt + id * (int64_t)be * D;
+  const int32_t* brows = rows + (int64_t)n * be;
+  const int tpr = D / VEC, rpi = 256 / tpr;
+  const int col = threadIdx.x % tpr, row0 = threadIdx.x / tpr;
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  constexpr int UR = 8;
+  for (int t0 = row0; t0 < be; t0 += UR * rpi) {
+    u32x4 raw[UR];
+#pragma unroll
+    for (int u = 0; u < UR; ++u) {
+      const int t = t0 + u * rpi;
+      raw[u] = u32x4{0u, 0u, 0u, 0u};
+      if (t < be) {
+        const int r = brows[t];
+        if (r >= 0 && r < s_out)
+          raw[u] = ld_stream(reinterpret_cast<const u32x4*>(src + (int64_t)r * D + col * VEC));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UR; ++u) {
+      const int t = t0 + u * rpi;
+      if (t >= be) break;
+      st_stream(reinterpret_cast<u32x4*>(dst + (int64_t)t * D + col * VEC), raw[u]);
+      if (t < valid) {
+        const T* vals = reinterpret_cast<const T*>(&raw[u]);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += Elem<T>::to_f(vals[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) part[row0 * D + col * VEC + e] = acc[e];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float s = 0.f;
+    for (int r = 0; r < rpi; ++r) s += part[r * D + d];
+    out[id * D + d] = Elem<T>::from_f(s / div);
+  }
+}
+
 constexpr int kMaxCoarseBlocks = 4096;  // generic kernels keep [2 Kb + D] fp32 rows in LDS
 
 // Generic coarse forward (fp32, or head dims the MFMA kernels do not take):
@@ -250,12 +324,19 @@ __device__ __forceinline__ void store_gate(G* __restrict__ p, const float* v) {
 // has element type G: T, or fp32 for an fp32 gate beside T inputs (its
 // gradient is then stored in fp32, as the reference stores it in the gate's
 // dtype, fused_common.py:202-221).
+// With RASTER, dout, the gate and d_gate are raster-order sequences of s_out
+// tokens: tiled slot n*be + t of a head is raster row rows[n*be + t] (< 0 for a
+// padding slot, whose dout and gate read as zero and which has no d_gate
+// row), and the pass also writes dout in the tiled layout (dout_t, zero rows
+// at the padding slots) for the fine backward kernels.  Every value is then
+// what the tiled pass computes after tile() of dout and of the gate.
 // ---------------------------------------------------------------------------
-template <typename T, typename G>
+template <typename T, typename G, bool RASTER = false>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const T* __restrict__ fine, const T* __restrict__ dout, const T* __restrict__ outc,
     const G* __restrict__ gate, int gate_mode, int gate_heads, float* __restrict__ delta,
-    T* __restrict__ d_outc, G* __restrict__ d_gate, int qb, int D, int be) {
+    T* __restrict__ d_outc, G* __restrict__ d_gate, int qb, int D, int be,
+    const int32_t* __restrict__ rows = nullptr, int64_t s_out = 0, T* __restrict__ dout_t = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float part[256 * VEC];
   const int64_t blk = blockIdx.x + (int64_t)blockIdx.y * qb;  // bh*qb + n
@@ -281,6 +362,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
   for (int t0 = row0; t0 < be; t0 += UR * rpi) {
     u32x4 ro[UR], rd[UR];
     float gv[UR][VEC];
+    int64_t rtok[UR];  // RASTER: raster token of row t (-1: padding slot)
 #pragma unroll
     for (int u = 0; u < UR; ++u) {
       const int t = t0 + u * rpi;
@@ -288,6 +370,27 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       const int64_t tok = blk * be + t;
       const int64_t off = tok * D + c0;
       ro[u] = ld_stream(reinterpret_cast<const u32x4*>(fine + off));
+      if constexpr (RASTER) {
+        const int r = rows[(int64_t)blockIdx.x * be + t];
+        rtok[u] = (r >= 0 && r < s_out) ? bh * s_out + r : -1;
+        const bool real = rtok[u] >= 0;
+        rd[u] = real ? ld_stream(reinterpret_cast<const u32x4*>(dout + rtok[u] * D + c0))
+                     : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(dout_t + off) = rd[u];
+        if (gate_mode == 1) {
+          if (real) {
+            load_gate<G, VEC>(gate + rtok[u] * D + c0, gv[u]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) gv[u][e] = 0.f;
+          }
+        } else {
+          const float gs = gate_mode == 2 ? (real ? Elem<G>::to_f(gate[rtok[u]]) : 0.f) : 1.f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) gv[u][e] = gs;
+        }
+        continue;
+      }
       rd[u] = ld_stream(reinterpret_cast<const u32x4*>(dout + off));
       if (gate_mode == 1 || gate_mode == 3) {
         // offset of this token's gate (and d_gate) chunk
@@ -322,10 +425,14 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
         }
       }
       if (outc && (gate_mode == 1 || gate_mode == 3)) {
-        const int64_t goff = gate_mode == 3
-                                 ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
-                                 : (blk * be + t) * D + c0;
-        store_gate<G, VEC>(d_gate + goff, dgv);
+        if constexpr (RASTER) {
+          if (rtok[u] >= 0) store_gate<G, VEC>(d_gate + rtok[u] * D + c0, dgv);
+        } else {
+          const int64_t goff = gate_mode == 3
+                                   ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
+                                   : (blk * be + t) * D + c0;
+          store_gate<G, VEC>(d_gate + goff, dgv);
+        }
       }
     }
     // reduce over the tpr lanes of each row (contiguous lanes)
@@ -343,7 +450,11 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
         if (t >= be) break;
         const int64_t tok = blk * be + t;
         delta[tok] = dl[u];
-        if (outc && gate_mode == 2) d_gate[tok] = Elem<G>::from_f(dg[u]);
+        if constexpr (RASTER) {
+          if (outc && gate_mode == 2 && rtok[u] >= 0) d_gate[rtok[u]] = Elem<G>::from_f(dg[u]);
+        } else {
+          if (outc && gate_mode == 2) d_gate[tok] = Elem<G>::from_f(dg[u]);
+        }
       }
     }
   }
@@ -522,6 +633,27 @@ extern "C" int vsa_pool_qkv(const void* q, const void* k, const void* v, const i
   return vsa_check_launch();
 }
 
+extern "C" int vsa_tile_pool_qkv(const void* q, const void* k, const void* v,
+                                 const int32_t* slot_rows, const int32_t* vbs, void* q_t,
+                                 void* k_t, void* v_t, void* q_c, void* k_c, void* v_c,
+                                 int64_t bh, int64_t s_out, int32_t nb, int32_t D, int32_t be,
+                                 int32_t dtype, void* stream) {
+  if (!q || !k || !v || !slot_rows || !vbs || !q_t || !k_t || !v_t || !q_c || !k_c || !v_c)
+    return VSA_ERR_NULL;
+  if (bh <= 0 || nb <= 0 || be <= 0 || be > 256 || s_out <= 0 || s_out > (int64_t)nb * be ||
+      !vec_dim_ok(D, dtype))
+    return VSA_ERR_SHAPE;
+  const int64_t grid = 3 * bh * nb;
+  if (grid > (1LL << 31) - 1) return VSA_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  VSA_DISPATCH_ALL(dtype, T, {
+    hipLaunchKernelGGL(tile_pool_kernel<T>, dim3((unsigned)grid), dim3(256), 0, s, (const T*)q,
+                       (const T*)k, (const T*)v, slot_rows, vbs, (T*)q_t, (T*)k_t, (T*)v_t,
+                       (T*)q_c, (T*)k_c, (T*)v_c, bh, nb, D, be, s_out);
+  });
+  return vsa_check_launch();
+}
+
 extern "C" int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c, float* scores,
                               float* probs, void* out_c, int32_t* selected, int64_t bh,
                               int32_t qb, int32_t kb, int32_t D, int32_t topk, float scale,
@@ -600,6 +732,30 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
       hipLaunchKernelGGL((bwd_prep_kernel<T, T>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
                          (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate,
                          gate_mode, gate_heads, delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
+  });
+  return vsa_check_launch();
+}
+
+extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const void* out_c,
+                                  const void* gate, int32_t gate_mode, const int32_t* slot_rows,
+                                  int64_t s_out, float* delta, void* d_out_c, void* d_gate,
+                                  void* dout_t, int64_t bh, int64_t sq, int32_t D, int32_t be,
+                                  int32_t dtype, void* stream) {
+  if (!fine_out || !dout || !delta || !slot_rows || !dout_t) return VSA_ERR_NULL;
+  if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;  // no token-major / fp32 gate here
+  if (out_c && !d_out_c) return VSA_ERR_NULL;
+  if (out_c && gate_mode != 0 && (!gate || !d_gate)) return VSA_ERR_NULL;
+  if (!out_c) gate_mode = 0;
+  if (bh <= 0 || be <= 0 || sq <= 0 || sq % be || s_out <= 0 || s_out > sq ||
+      !vec_dim_ok(D, dtype))
+    return VSA_ERR_SHAPE;
+  const int qb = (int)(sq / be);
+  hipStream_t s = (hipStream_t)stream;
+  VSA_DISPATCH_ALL(dtype, T, {
+    hipLaunchKernelGGL((bwd_prep_kernel<T, T, true>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
+                       (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate,
+                       gate_mode, 1, delta, (T*)d_out_c, (T*)d_gate, qb, D, be, slot_rows, s_out,
+                       (T*)dout_t);
   });
   return vsa_check_launch();
 }

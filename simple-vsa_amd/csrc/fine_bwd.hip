@@ -40,14 +40,22 @@ struct DqCfg {
 
 // dQ epilogue: scale, fold the pooled gradient of the query block
 // (`d_q_c / count`, valid rows only), store.  One lane = one query row,
-// holding dQ^T column r.
-template <typename T, int D, int BE>
+// holding dQ^T column r.  With RASTER, dq is a raster-order sequence of s_out
+// tokens: slot myq goes to raster row orows[myq], a padding slot (< 0) nowhere.
+template <typename T, int D, int BE, bool RASTER = false>
 __device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64_t b, int myq,
                                             int qblk, int h, int sq, int qb, T* __restrict__ dq,
                                             const T* __restrict__ dqc,
-                                            const int32_t* __restrict__ q_vbs, float scale) {
+                                            const int32_t* __restrict__ q_vbs, float scale,
+                                            const int32_t* __restrict__ orows = nullptr,
+                                            int64_t s_out = 0) {
   using E = Elem<T>;
-  const int64_t tok = (int64_t)b * sq + myq;
+  int64_t tok = (int64_t)b * sq + myq;
+  if constexpr (RASTER) {
+    const int r = orows[myq];
+    if (r < 0 || r >= s_out) return;
+    tok = (int64_t)b * s_out + r;
+  }
   const int qpos = myq - qblk * BE;
   float cdiv = 1.f;
   bool cvalid = false;
@@ -89,7 +97,7 @@ __device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64
   }
 }
 
-template <typename T, int D, int BE>
+template <typename T, int D, int BE, bool RASTER>
 __global__ __launch_bounds__((DqCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(DqCfg<D, BE>::WPE))) void
 sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
                  const T* __restrict__ dout, const float* __restrict__ lse,
@@ -97,7 +105,7 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
                  const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
                  const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
                  int tiles_per_head, int sq, int skv, int qb, int kb, int topk, float c2,
-                 uint32_t qsign, float scale) {
+                 uint32_t qsign, float scale, const int32_t* __restrict__ orows, int64_t s_out) {
   using C = DqCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
@@ -202,7 +210,8 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
   }
 
-  dq_epilogue<T, D, BE>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale);
+  dq_epilogue<T, D, BE, RASTER>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale, orows,
+                                s_out);
 }
 
 // ===========================================================================
@@ -252,7 +261,7 @@ struct DkvShared {
 // One key tile (tile_s < num_tiles) of sparse_dkdv_kernel, start to finish.
 // On return every wave's direct loads may still be in flight (the last steps
 // re-copy the last item): the caller drains them before the LDS is reused.
-template <typename T, int D, int BE>
+template <typename T, int D, int BE, bool RASTER>
 __device__ __forceinline__ void dkdv_tile(
     DkvShared<T, D, BE>& sh, int tile_s,
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -261,7 +270,8 @@ __device__ __forceinline__ void dkdv_tile(
     const int32_t* __restrict__ inverse, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ dk, T* __restrict__ dv, const T* __restrict__ dkc,
     const T* __restrict__ dvc, int tiles_per_head, int sq, int skv, int qb,
-    int kb, int topk, float c2, uint32_t ksign, float scale) {
+    int kb, int topk, float c2, uint32_t ksign, float scale,
+    const int32_t* __restrict__ orows, int64_t s_out) {
   using C = DkvCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
@@ -547,6 +557,14 @@ __device__ __forceinline__ void dkdv_tile(
 
 epilogue:
   // ---- epilogue ------------------------------------------------------------
+  // dK / dV row: this key's slot, or with RASTER its raster row orows[mykey]
+  // in a sequence of s_out tokens (a padding slot, < 0, has none)
+  int64_t otok = ktok;
+  if constexpr (RASTER) {
+    const int r = orows[mykey];
+    otok = (r >= 0 && r < s_out) ? (int64_t)b * s_out + r : -1;
+  }
+  const bool ostore = !RASTER || otok >= 0;
   const float cdiv = (float)(cnt > 1 ? cnt : 1), rcp = 1.0f / cdiv;
   const T* kcrow = dkc ? dkc + ((int64_t)b * kb + kvblk) * D : nullptr;
   const T* vcrow = dvc ? dvc + ((int64_t)b * kb + kvblk) * D : nullptr;
@@ -589,8 +607,10 @@ epilogue:
         k4[e] = E::from_f(fk + ck[e]);
         v4[e] = E::from_f(fv + cv[e]);
       }
-      *reinterpret_cast<u32x2*>(dk + ktok * D + d0) = *reinterpret_cast<const u32x2*>(k4);
-      *reinterpret_cast<u32x2*>(dv + ktok * D + d0) = *reinterpret_cast<const u32x2*>(v4);
+      if (ostore) {
+        *reinterpret_cast<u32x2*>(dk + otok * D + d0) = *reinterpret_cast<const u32x2*>(k4);
+        *reinterpret_cast<u32x2*>(dv + otok * D + d0) = *reinterpret_cast<const u32x2*>(v4);
+      }
     }
   }
 }
@@ -604,7 +624,7 @@ epilogue:
 // tiles) and the last workgroup to finish zeroes the counters for the next
 // launch; without one, a fixed stride over the range in index order.  Head
 // dim 256 keeps one workgroup per tile (tile_order[i] or the XCD order).
-template <typename T, int D, int BE>
+template <typename T, int D, int BE, bool RASTER>
 __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -612,16 +632,17 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     const int32_t* __restrict__ inverse, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ dk, T* __restrict__ dv, const T* __restrict__ dkc,
     const T* __restrict__ dvc, int num_tiles, int tiles_per_head, int sq, int skv, int qb,
-    int kb, int topk, float c2, uint32_t ksign, float scale, int32_t* __restrict__ tile_order) {
+    int kb, int topk, float c2, uint32_t ksign, float scale, int32_t* __restrict__ tile_order,
+    const int32_t* __restrict__ orows, int64_t s_out) {
   __shared__ DkvShared<T, D, BE> sh;
   if constexpr (DkvCfg<D, BE>::NSPLIT > 1) {
     // head_dim 256: one tile per workgroup (the loop's state would push the
     // fragments and accumulators, which fill the register file, into scratch)
     const int tile_s = tile_order ? tile_order[blockIdx.x] : xcd_tile(blockIdx.x, num_tiles);
     if (tile_s < num_tiles)
-      dkdv_tile<T, D, BE>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets, inverse,
-                          kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb, kb, topk, c2,
-                          ksign, scale);
+      dkdv_tile<T, D, BE, RASTER>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets,
+                                  inverse, kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb,
+                                  kb, topk, c2, ksign, scale, orows, s_out);
     return;
   }
   __shared__ int s_next;
@@ -641,9 +662,9 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     if (j >= per) break;
     const int tile_s = ctr ? tile_order[xcd + 8 * j] : xcd * per + j;
     if (tile_s < num_tiles)
-      dkdv_tile<T, D, BE>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets, inverse,
-                          kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb, kb, topk, c2,
-                          ksign, scale);
+      dkdv_tile<T, D, BE, RASTER>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets,
+                                  inverse, kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb,
+                                  kb, topk, c2, ksign, scale, orows, s_out);
     dma_wait();       // this wave's trailing copies land before the LDS is reused
     __syncthreads();  // and every wave is done with it (and with s_next)
   }
@@ -677,14 +698,14 @@ struct DqPPCfg {
 };
 
 // One query block (tile < bh * Sq / 256) of sparse_dq_pp_kernel.
-template <typename T, int D>
+template <typename T, int D, bool RASTER>
 __device__ __forceinline__ void dq_pp_tile(
     T* smem, int tile, const T* __restrict__ q, const T* __restrict__ k,
     const T* __restrict__ v, const T* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta, const int32_t* __restrict__ selected,
     const int32_t* __restrict__ kv_vbs, T* __restrict__ dq, const T* __restrict__ dqc,
     const int32_t* __restrict__ q_vbs, int sq, int skv, int qb, int kb, int topk, float c2,
-    uint32_t qsign, float scale) {
+    uint32_t qsign, float scale, const int32_t* __restrict__ orows, int64_t s_out) {
   constexpr int BE = 256;
   using C = DqPPCfg<D>;
   using E = Elem<T>;
@@ -923,11 +944,12 @@ __device__ __forceinline__ void dq_pp_tile(
     }
   }
   if (!grp1) phase_barrier();
-  dq_epilogue<T, D, BE>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale);
+  dq_epilogue<T, D, BE, RASTER>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale, orows,
+                                s_out);
 }
 
 // Persistent, with the query-block walk of sparse_fwd_pp_kernel.
-template <typename T, int D>
+template <typename T, int D, bool RASTER>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
                     const T* __restrict__ dout, const float* __restrict__ lse,
@@ -935,65 +957,65 @@ sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
                     const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
                     const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
-                    float scale) {
+                    float scale, const int32_t* __restrict__ orows, int64_t s_out) {
   using C = DqPPCfg<D>;
   __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
   const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
   for (int j = (int)(blockIdx.x >> 3); j < per; j += stride) {
     const int tile = xcd * per + j;
     if (tile >= num_tiles) break;
-    dq_pp_tile<T, D>(smem, tile, q, k, v, dout, lse, delta, selected, kv_vbs, dq, dqc, q_vbs, sq,
-                     skv, qb, kb, topk, c2, qsign, scale);
+    dq_pp_tile<T, D, RASTER>(smem, tile, q, k, v, dout, lse, delta, selected, kv_vbs, dq, dqc,
+                             q_vbs, sq, skv, qb, kb, topk, c2, qsign, scale, orows, s_out);
     dma_wait();
     __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool RASTER = false>
 static int launch_dq_pp(const void* q, const void* k, const void* v, const void* dout,
                         const float* lse, const float* delta, const int32_t* selected,
                         const int32_t* kv_vbs, void* dq, const void* dqc, const int32_t* q_vbs,
                         int64_t bh, int64_t sq, int64_t skv, int topk, float scale,
-                        hipStream_t stream) {
+                        hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0) {
   const int64_t tiles = bh * (sq / 256);
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   const int64_t want = ((tiles + 7) / 8) * 8;
   const int resident = (cu_count() / 8) * 8;  // one 8-wave workgroup per CU
   const int grid = (int)(want < resident ? want : resident);
-  hipLaunchKernelGGL((sparse_dq_pp_kernel<T, D>), dim3(grid), dim3(512), 0, stream,
+  hipLaunchKernelGGL((sparse_dq_pp_kernel<T, D, RASTER>), dim3(grid), dim3(512), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, selected,
                      kv_vbs, (T*)dq, (const T*)dqc, q_vbs, (int)tiles, (int)sq, (int)skv,
                      (int)(sq / 256), (int)(skv / 256), topk, fabsf(scale) * kLog2e,
-                     scale < 0.f ? 0x80008000u : 0u, scale);
+                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out);
   return vsa_check_launch();
 }
 
-template <typename T, int D, int BE>
+template <typename T, int D, int BE, bool RASTER = false>
 static int launch_dq(const void* q, const void* k, const void* v, const void* dout,
                      const float* lse, const float* delta, const int32_t* selected,
                      const int32_t* kv_vbs, void* dq, const void* dqc, const int32_t* q_vbs,
                      int64_t bh, int64_t sq, int64_t skv, int topk, float scale,
-                     hipStream_t stream) {
+                     hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0) {
   using C = DqCfg<D, BE>;
   const int tph = (int)(sq / C::QT);
   const int64_t tiles = bh * tph;
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   const int grid = (int)(((tiles + 7) / 8) * 8);
-  hipLaunchKernelGGL((sparse_dq_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
+  hipLaunchKernelGGL((sparse_dq_kernel<T, D, BE, RASTER>), dim3(grid), dim3(C::NT), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, selected,
                      kv_vbs, (T*)dq, (const T*)dqc, q_vbs, (int)tiles, tph, (int)sq, (int)skv,
                      (int)(sq / BE), (int)(skv / BE), topk, fabsf(scale) * kLog2e,
-                     scale < 0.f ? 0x80008000u : 0u, scale);
+                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out);
   return vsa_check_launch();
 }
 
-template <typename T, int D, int BE>
+template <typename T, int D, int BE, bool RASTER = false>
 static int launch_dkdv(const void* q, const void* k, const void* v, const void* dout,
                        const float* lse, const float* delta, const int32_t* counts,
                        const int32_t* offsets, const int32_t* inverse, const int32_t* kv_vbs,
                        void* dk, void* dv, const void* dkc, const void* dvc, int64_t bh,
                        int64_t sq, int64_t skv, int topk, float scale, int32_t* tile_order,
-                       hipStream_t stream) {
+                       hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0) {
   using C = DkvCfg<D, BE>;
   const int tph = (int)(skv / C::KT);
   const int64_t tiles = bh * tph * C::NSPLIT;
@@ -1003,11 +1025,12 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
   const int resident = cu_count() * (4 / C::NW);
   const int64_t want = ((tiles + 7) / 8) * 8;
   const int grid = C::NSPLIT > 1 || want < resident ? (int)want : (resident / 8) * 8;
-  hipLaunchKernelGGL((sparse_dkdv_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
+  hipLaunchKernelGGL((sparse_dkdv_kernel<T, D, BE, RASTER>), dim3(grid), dim3(C::NT), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, counts,
                      offsets, inverse, kv_vbs, (T*)dk, (T*)dv, (const T*)dkc, (const T*)dvc,
                      (int)tiles, tph, (int)sq, (int)skv, (int)(sq / BE), (int)(skv / BE), topk,
-                     fabsf(scale) * kLog2e, scale < 0.f ? 0x80008000u : 0u, scale, tile_order);
+                     fabsf(scale) * kLog2e, scale < 0.f ? 0x80008000u : 0u, scale, tile_order,
+                     orows, s_out);
   return vsa_check_launch();
 }
 
@@ -1264,4 +1287,70 @@ extern "C" int vsa_sparse_bwd_dkdv_noalloc(const void* q, const void* k, const v
   return vsa_sparse_bwd_dkdv(q, k, v, dout, lse, delta, counts, offsets, inverse, kv_vbs, dk,
                              dv, d_k_c, d_v_c, bh, sq, skv, D, be, topk, scale, order, dtype,
                              stream);
+}
+
+// ---------------------------------------------------------------------------
+// Tiled-sequence variants: q, k, v, dout in the padded tile layout (as the
+// forward's tile pass wrote them), dq / dk / dv written straight to a
+// raster-order sequence of s_out tokens through slot_rows (tiled slot ->
+// raster row, -1 for a padding slot), which is what untile() of the tiled
+// gradients would produce for the real tokens.  bf16 / fp16, head dims 64 and
+// 128, blocks of 64, 128 and 256 tokens.
+// ---------------------------------------------------------------------------
+#define VSA_TILED_SHAPES(X) X(128, 256) X(128, 128) X(128, 64) X(64, 256) X(64, 128) X(64, 64)
+
+extern "C" int vsa_sparse_bwd_dq_tiled(const void* q, const void* k, const void* v,
+                                       const void* dout, const float* lse, const float* delta,
+                                       const int32_t* selected, const int32_t* kv_vbs, void* dq,
+                                       const void* d_q_c, const int32_t* q_vbs,
+                                       const int32_t* slot_rows, int64_t s_out, int64_t bh,
+                                       int64_t sq, int64_t skv, int32_t D, int32_t be,
+                                       int32_t topk, float scale, int32_t dtype, void* stream) {
+  if (!q || !k || !v || !dout || !lse || !delta || !selected || !kv_vbs || !dq || !slot_rows)
+    return VSA_ERR_NULL;
+  if (d_q_c && !q_vbs) return VSA_ERR_NULL;
+  if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
+      s_out <= 0 || s_out > sq || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
+    return VSA_ERR_SHAPE;
+  if (dtype != VSA_BF16 && dtype != VSA_F16) return dtype == VSA_F32 ? VSA_ERR_UNSUPPORTED : VSA_ERR_DTYPE;
+  hipStream_t s = (hipStream_t)stream;
+#define VSA_DQ_TILED_CASE(DD, BB)                                                            \
+  if (D == DD && be == BB) {                                                                 \
+    if (BB == 256 && bh * (sq / 256) >= 256)                                                 \
+      return launch_dq_pp<T, DD, true>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, \
+                                       q_vbs, bh, sq, skv, topk, scale, s, slot_rows, s_out); \
+    return launch_dq<T, DD, BB, true>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, \
+                                      q_vbs, bh, sq, skv, topk, scale, s, slot_rows, s_out);  \
+  }
+  VSA_DISPATCH_MFMA(dtype, T, { VSA_TILED_SHAPES(VSA_DQ_TILED_CASE) });
+#undef VSA_DQ_TILED_CASE
+  return VSA_ERR_UNSUPPORTED;
+}
+
+extern "C" int vsa_sparse_bwd_dkdv_tiled(const void* q, const void* k, const void* v,
+                                         const void* dout, const float* lse, const float* delta,
+                                         const int32_t* counts, const int32_t* offsets,
+                                         const int32_t* inverse, const int32_t* kv_vbs, void* dk,
+                                         void* dv, const void* d_k_c, const void* d_v_c,
+                                         const int32_t* slot_rows, int64_t s_out, int64_t bh,
+                                         int64_t sq, int64_t skv, int32_t D, int32_t be,
+                                         int32_t topk, float scale, int32_t* tile_order,
+                                         int32_t dtype, void* stream) {
+  if (!q || !k || !v || !dout || !lse || !delta || !counts || !offsets || !inverse || !kv_vbs ||
+      !dk || !dv || !slot_rows)
+    return VSA_ERR_NULL;
+  if ((d_k_c == nullptr) != (d_v_c == nullptr)) return VSA_ERR_NULL;
+  if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
+      s_out <= 0 || s_out > skv || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
+    return VSA_ERR_SHAPE;
+  if (dtype != VSA_BF16 && dtype != VSA_F16) return dtype == VSA_F32 ? VSA_ERR_UNSUPPORTED : VSA_ERR_DTYPE;
+  hipStream_t s = (hipStream_t)stream;
+#define VSA_DKDV_TILED_CASE(DD, BB)                                                          \
+  if (D == DD && be == BB)                                                                   \
+    return launch_dkdv<T, DD, BB, true>(q, k, v, dout, lse, delta, counts, offsets, inverse, \
+                                        kv_vbs, dk, dv, d_k_c, d_v_c, bh, sq, skv, topk,     \
+                                        scale, tile_order, s, slot_rows, s_out);
+  VSA_DISPATCH_MFMA(dtype, T, { VSA_TILED_SHAPES(VSA_DKDV_TILED_CASE) });
+#undef VSA_DKDV_TILED_CASE
+  return VSA_ERR_UNSUPPORTED;
 }

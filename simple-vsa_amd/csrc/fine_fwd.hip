@@ -46,25 +46,35 @@ struct FwdCfg {
 constexpr float kRescaleSlack = 8.0f;  // log2 units
 
 // Normalise, fused combine, store, LSE (one lane = one query row, holding
-// O^T column r and a partial row sum).
-template <typename T, int D>
+// O^T column r and a partial row sum).  With RASTER the combined output and
+// the gate are rows of a raster-order sequence of s_out tokens: slot myq of
+// the tiled layout is raster row orows[myq] (< 0 for a padding slot, which
+// has no output row); the fine output and the LSE stay in the tiled layout.
+template <typename T, int D, bool RASTER = false>
 __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float lsum, float m,
                                              int64_t b, int myq, int qblk, int h, int sq, int qb,
                                              T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse,
                                              const T* __restrict__ outc,
                                              const T* __restrict__ gate, int gate_mode,
-                                             int gate_heads) {
+                                             int gate_heads, const int32_t* __restrict__ orows = nullptr,
+                                             int64_t s_out = 0) {
   using E = Elem<T>;
   const float ltot = pair_sum32(lsum);
   const float inv = 1.0f / ltot;
   const int64_t tok = (int64_t)b * sq + myq;
+  int64_t otok = tok;  // row of the combined output and of the gate
+  if constexpr (RASTER) {
+    const int r = orows[myq];
+    otok = (r >= 0 && r < s_out) ? (int64_t)b * s_out + r : -1;
+  }
+  const bool ostore = !RASTER || otok >= 0;
   const T* ocrow = outc ? outc + ((int64_t)b * qb + qblk) * D : nullptr;
   float gtok = 1.f;
-  if (outc && gate_mode == 2) gtok = E::to_f(gate[tok]);
+  if (outc && gate_mode == 2 && ostore) gtok = E::to_f(gate[otok]);
   // gate row of this token: [BH, Sq, D] (mode 1) or token-major [B, Sq, H, D] (mode 3)
   const T* grow = nullptr;
-  if (gate_mode == 1) grow = gate + tok * D;
-  if (gate_mode == 3)
+  if (gate_mode == 1 && ostore) grow = gate + otok * D;
+  if (!RASTER && gate_mode == 3)
     grow = gate + (((int64_t)(b / gate_heads) * sq + myq) * gate_heads + b % gate_heads) * D;
   // the combine operands are loaded together, so their latency is paid once
   u32x2 ocr[D / 32][4], gr[D / 32][4];
@@ -104,7 +114,7 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
       T o4[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) o4[e] = E::from_f(val[e]);
-      *reinterpret_cast<u32x2*>(out + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
+      if (ostore) *reinterpret_cast<u32x2*>(out + otok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
     }
   }
   if (ocrow && fine) {  // the fine output as stored in T, for the backward's delta
@@ -124,13 +134,14 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
   if (lse != nullptr && h == 0) lse[tok] = m + log2f(ltot);
 }
 
-template <typename T, int D, int BE>
+template <typename T, int D, int BE, bool RASTER>
 __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(FwdCfg<D, BE>::WPE))) void sparse_fwd_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
     const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles, int tiles_per_head, int sq,
-    int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
+    int skv, int qb, int kb, int topk, float c2, uint32_t qsign, const int32_t* __restrict__ orows,
+    int64_t s_out) {
   using C = FwdCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
@@ -265,8 +276,8 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
   }
 
-  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate, gate_mode,
-                     gate_heads);
+  fwd_epilogue<T, D, RASTER>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate,
+                             gate_mode, gate_heads, orows, s_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -294,13 +305,13 @@ struct FwdPPCfg {
 };
 
 // One query block (tile < bh * Sq / 256) of sparse_fwd_pp_kernel.
-template <typename T, int D>
+template <typename T, int D, bool RASTER>
 __device__ __forceinline__ void fwd_pp_tile(
     T* smem, int tile, const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
     const T* __restrict__ gate, int gate_mode, int gate_heads, int sq, int skv, int qb, int kb,
-    int topk, float c2, uint32_t qsign) {
+    int topk, float c2, uint32_t qsign, const int32_t* __restrict__ orows, int64_t s_out) {
   constexpr int BE = 256;
   using C = FwdPPCfg<D>;
   using E = Elem<T>;
@@ -609,39 +620,41 @@ __device__ __forceinline__ void fwd_pp_tile(
     }
   }
   if (!grp1) phase_barrier();
-  fwd_epilogue<T, D>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate, gate_mode,
-                     gate_heads);
+  fwd_epilogue<T, D, RASTER>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate,
+                             gate_mode, gate_heads, orows, s_out);
 }
 
 // Persistent: as many workgroups as the CUs hold (one each), every query block
 // has the same topk chunks, so a fixed stride balances them.  Workgroup i runs
 // on XCD i % 8 and walks that XCD's contiguous range of query blocks (the
 // xcd_tile order), so one head's K/V stay in one XCD's L2.
-template <typename T, int D>
+template <typename T, int D, bool RASTER>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
                      const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
                      T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
                      const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles,
-                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign) {
+                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
+                     const int32_t* __restrict__ orows, int64_t s_out) {
   using C = FwdPPCfg<D>;
   __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
   const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
   for (int j = (int)(blockIdx.x >> 3); j < per; j += stride) {
     const int tile = xcd * per + j;
     if (tile >= num_tiles) break;
-    fwd_pp_tile<T, D>(smem, tile, q, k, v, selected, kv_vbs, out, fine, lse, outc, gate, gate_mode,
-                      gate_heads, sq, skv, qb, kb, topk, c2, qsign);
+    fwd_pp_tile<T, D, RASTER>(smem, tile, q, k, v, selected, kv_vbs, out, fine, lse, outc, gate,
+                              gate_mode, gate_heads, sq, skv, qb, kb, topk, c2, qsign, orows, s_out);
     dma_wait();
     __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool RASTER = false>
 static int launch_fwd_pp(const void* q, const void* k, const void* v, const int32_t* selected,
                          const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* outc,
                          const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq,
-                         int64_t skv, int topk, float scale, hipStream_t stream) {
+                         int64_t skv, int topk, float scale, hipStream_t stream,
+                         const int32_t* orows = nullptr, int64_t s_out = 0) {
   const int64_t tiles = bh * (sq / 256);
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   const int64_t want = ((tiles + 7) / 8) * 8;
@@ -649,18 +662,19 @@ static int launch_fwd_pp(const void* q, const void* k, const void* v, const int3
   const int grid = (int)(want < resident ? want : resident);
   const float c2 = fabsf(scale) * kLog2e;
   const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
-  hipLaunchKernelGGL((sparse_fwd_pp_kernel<T, D>), dim3(grid), dim3(512), 0, stream,
+  hipLaunchKernelGGL((sparse_fwd_pp_kernel<T, D, RASTER>), dim3(grid), dim3(512), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, (T*)fine, lse,
                      (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, (int)sq,
-                     (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign);
+                     (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign, orows, s_out);
   return vsa_check_launch();
 }
 
-template <typename T, int D, int BE>
+template <typename T, int D, int BE, bool RASTER = false>
 static int launch_fwd(const void* q, const void* k, const void* v, const int32_t* selected,
                       const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* outc,
                       const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq, int64_t skv,
-                      int topk, float scale, hipStream_t stream) {
+                      int topk, float scale, hipStream_t stream, const int32_t* orows = nullptr,
+                      int64_t s_out = 0) {
   using C = FwdCfg<D, BE>;
   const int tph = (int)(sq / C::QT);
   const int64_t tiles = bh * tph;
@@ -668,10 +682,10 @@ static int launch_fwd(const void* q, const void* k, const void* v, const int32_t
   const int grid = (int)(((tiles + 7) / 8) * 8);
   const float c2 = fabsf(scale) * kLog2e;
   const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
-  hipLaunchKernelGGL((sparse_fwd_kernel<T, D, BE>), dim3(grid), dim3(C::NT), 0, stream,
+  hipLaunchKernelGGL((sparse_fwd_kernel<T, D, BE, RASTER>), dim3(grid), dim3(C::NT), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, (T*)fine, lse,
                      (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, tph, (int)sq,
-                     (int)skv, (int)(sq / BE), (int)(skv / BE), topk, c2, qsign);
+                     (int)skv, (int)(sq / BE), (int)(skv / BE), topk, c2, qsign, orows, s_out);
   return vsa_check_launch();
 }
 
@@ -741,6 +755,47 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
     VSA_FWD_CASE(64, 256)
     VSA_FWD_CASE(64, 128)
     VSA_FWD_CASE(64, 64)
+  });
+  return VSA_ERR_UNSUPPORTED;
+}
+
+#define VSA_FWD_TILED_CASE(DD, BB)                                                             \
+  if (D == DD && be == BB) {                                                                   \
+    if (BB == 256 && bh * (sq / 256) >= 256)                                                   \
+      return launch_fwd_pp<T, DD, true>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c,  \
+                                        gate, gate_mode, 0, bh, sq, skv, topk, scale, s,       \
+                                        slot_rows, s_out);                                     \
+    return launch_fwd<T, DD, BB, true>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c,   \
+                                       gate, gate_mode, 0, bh, sq, skv, topk, scale, s,        \
+                                       slot_rows, s_out);                                      \
+  }
+
+extern "C" int vsa_sparse_fwd_tiled(const void* q, const void* k, const void* v,
+                                    const int32_t* selected, const int32_t* kv_vbs, void* out,
+                                    void* fine_out, float* lse, const void* out_c,
+                                    const void* gate, int32_t gate_mode,
+                                    const int32_t* slot_rows, int64_t s_out, int64_t bh,
+                                    int64_t sq, int64_t skv, int32_t D, int32_t be, int32_t topk,
+                                    float scale, int32_t dtype, void* stream) {
+  if (!q || !k || !v || !selected || !kv_vbs || !out || !slot_rows) return VSA_ERR_NULL;
+  if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;  // no token-major / fp32 gate here
+  if (out_c && gate_mode != 0 && !gate) return VSA_ERR_NULL;
+  if (!out_c) {
+    gate_mode = 0;
+    fine_out = nullptr;
+  }
+  if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
+      s_out <= 0 || s_out > sq || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
+    return VSA_ERR_SHAPE;
+  if (dtype == VSA_F32) return VSA_ERR_UNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
+  VSA_DISPATCH_MFMA(dtype, T, {
+    VSA_FWD_TILED_CASE(128, 256)
+    VSA_FWD_TILED_CASE(128, 128)
+    VSA_FWD_TILED_CASE(128, 64)
+    VSA_FWD_TILED_CASE(64, 256)
+    VSA_FWD_TILED_CASE(64, 128)
+    VSA_FWD_TILED_CASE(64, 64)
   });
   return VSA_ERR_UNSUPPORTED;
 }

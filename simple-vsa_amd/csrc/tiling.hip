@@ -55,6 +55,31 @@ __global__ void tile_metadata_kernel(int T, int H, int W, int ts, int hs, int ws
   }
 }
 
+// Inverse map for the fused tiled op: slot p of tile n (padded layout, tile
+// volume be) holds raster token
+//   r = ((nt*ts + dt)*H + nh*hs + dh)*W + nw*ws + dw,
+// (dt, dh, dw) = (p / (eh*ew), (p / ew) % eh, p % ew), for p < et*eh*ew, and
+// nothing (-1) after that.
+__global__ void tile_slot_rows_kernel(int T, int H, int W, int ts, int hs, int ws, int NH, int NW,
+                                      int be, int64_t slots, int32_t* __restrict__ rows) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= slots) return;
+  const int64_t n = g / be;
+  const int p = (int)(g - n * be);
+  const int nw = (int)(n % NW);
+  const int64_t rest = n / NW;
+  const int nh = (int)(rest % NH);
+  const int nt = (int)(rest / NH);
+  const int et = min(ts, T - nt * ts), eh = min(hs, H - nh * hs), ew = min(ws, W - nw * ws);
+  const int hw = eh * ew;
+  if (p >= et * hw) {
+    rows[g] = -1;
+    return;
+  }
+  const int dt = p / hw, dh = (p - dt * hw) / ew, dw = p - dt * hw - dh * ew;
+  rows[g] = (int32_t)(((int64_t)(nt * ts + dt) * H + nh * hs + dh) * W + nw * ws + dw);
+}
+
 // index of item i through an optional second level: outer ? a[outer[i]] : (a ? a[i] : i);
 // -1 when a lookup would leave its table
 __device__ __forceinline__ int64_t lookup(const int64_t* __restrict__ a, int64_t a_len,
@@ -181,6 +206,22 @@ extern "C" int vsa_tile_metadata(int32_t T, int32_t H, int32_t W, int32_t ts, in
                      (hipStream_t)stream, T, H, W, ts, hs, ws, NH, NW, (int)be, S, nb,
                      tile_partition_indices, reverse_indices, non_pad_index,
                      variable_block_sizes);
+  return vsa_check_launch();
+}
+
+extern "C" int vsa_tile_slot_rows(int32_t T, int32_t H, int32_t W, int32_t ts, int32_t hs,
+                                  int32_t ws, int32_t* slot_rows, void* stream) {
+  if (!slot_rows) return VSA_ERR_NULL;
+  if (T <= 0 || H <= 0 || W <= 0 || ts <= 0 || hs <= 0 || ws <= 0) return VSA_ERR_SHAPE;
+  const int64_t S = (int64_t)T * H * W;
+  const int NT = (T + ts - 1) / ts, NH = (H + hs - 1) / hs, NW = (W + ws - 1) / ws;
+  const int64_t be = (int64_t)ts * hs * ws;
+  const int64_t slots = (int64_t)NT * NH * NW * be;
+  if (S >= (1LL << 31) || be > (1LL << 20) || slots > (1LL << 40) ||
+      (slots + 255) / 256 > 0x7fffffffLL)
+    return VSA_ERR_SHAPE;
+  hipLaunchKernelGGL(tile_slot_rows_kernel, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, T, H, W, ts, hs, ws, NH, NW, (int)be, slots, slot_rows);
   return vsa_check_launch();
 }
 

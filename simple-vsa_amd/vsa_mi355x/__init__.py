@@ -17,7 +17,7 @@ from .gate import CompressionGate
 from .tiling import build_vsa_metadata, tile, untile
 
 __all__ = ["mi355x_vsa", "mi355x_sparse_attention", "mi355x_sparse_executor", "mi355x_route",
-           "CompressionGate", "build_vsa_metadata", "tile", "untile"]
+           "mi355x_vsa_tiled", "CompressionGate", "build_vsa_metadata", "tile", "untile"]
 
 
 def mi355x_vsa(*args: Any, **kwargs: Any) -> Any:
@@ -44,5 +44,13 @@ def mi355x_sparse_executor(*args: Any, **kwargs: Any) -> Any:
 def mi355x_route(*args: Any, **kwargs: Any) -> Any:
     """Coarse scores and Top-K route that ``mi355x_vsa`` uses."""
     from .mi355x import mi355x_route as _impl
+
+    return _impl(*args, **kwargs)
+
+
+def mi355x_vsa_tiled(*args: Any, **kwargs: Any) -> Any:
+    """VSA on raster-order video tokens with tile / untile fused into the op;
+    see ``vsa_mi355x.tiled``."""
+    from .tiled import mi355x_vsa_tiled as _impl
 
     return _impl(*args, **kwargs)

@@ -501,8 +501,10 @@ def _prepare_gate(gate: Optional[Tensor], q: Tensor) -> Optional[Tensor]:
     full = (b, h, s, 1) if per_token else (b, h, s, d)
     if gate.dtype != q.dtype or tuple(gate.shape) != full:
         gate = gate.float().expand(full)
-    # the gate producer's per-head view of its [B, S, H, D] output is consumed in place
-    return gate if _token_major(gate) else gate.contiguous()
+    # the gate producer's per-head view of its [B, S, H, D] output is consumed in
+    # place; a per-token gate is always read as contiguous [B*H, S] (a transposed
+    # [B, S, H, 1] view has the token-major strides too, so it must be copied)
+    return gate if (not per_token and _token_major(gate)) else gate.contiguous()
 
 
 def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,

@@ -1,0 +1,202 @@
+"""VSA on raster-order video tokens, with tile() / untile() fused into the op.
+
+A video DiT keeps its tokens in raster order (t, h, w) and, for VSA, moves
+them into the padded tile-contiguous layout before the op and back after it
+(the reference's ``tile`` / ``untile``, fastvideo_tiling.py:130-145): two full
+passes over q, k, v and the gate before the op, one over the output after it,
+and the same again for the gradients.  ``mi355x_vsa_tiled`` runs the op on
+raster-order tensors instead:
+
+* forward: one pass reads raster q, k, v and writes both their tiled copies
+  and the block means (``vsa_tile_pool_qkv``); the fine forward writes the
+  combined output at raster rows and reads the gate there
+  (``vsa_sparse_fwd_tiled``);
+* backward: the preprocessing pass reads raster dout and gate, writes d_gate
+  at raster rows and the tiled dout the fine kernels consume
+  (``vsa_bwd_prep_tiled``); the dQ and dK/dV epilogues store at raster rows.
+
+Every value equals ``untile(mi355x_vsa(tile(q), tile(k), tile(v), ...))`` bit
+for bit.  Shapes or dtypes without a fused kernel (fp32, head dims other than
+64 / 128, tile volumes other than 64 / 128 / 256, a gate that is not
+``[B, H, S, D]`` or ``[B, H, S, 1]`` in q's dtype) run that composition.
+"""
+
+from __future__ import annotations
+
+import functools
+import math
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from . import mi355x as M
+from . import tiling
+
+FUSED_BLOCKS = (64, 128, 256)
+FUSED_HEAD_DIMS = (64, 128)
+
+
+@functools.lru_cache(maxsize=16)
+def _slot_rows(shape: Tuple[int, int, int], tile_size: Tuple[int, int, int],
+               device: torch.device) -> Tensor:
+    """int32 [nb * be]: raster token of each padded tile slot, -1 for padding."""
+    T, H, W = shape
+    ts, hs, ws = tile_size
+    nb = math.ceil(T / ts) * math.ceil(H / hs) * math.ceil(W / ws)
+    rows = torch.empty(nb * ts * hs * ws, dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        _lib.call("vsa_tile_slot_rows", T, H, W, ts, hs, ws, _lib.ptr(rows),
+                  _lib.stream_of(rows))
+    return rows
+
+
+def slot_rows(dit_seq_shape, tile_size, device) -> Tensor:
+    """The slot -> raster-token table of a latent grid (cached per device)."""
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    return _slot_rows(tuple(int(x) for x in dit_seq_shape), tuple(int(x) for x in tile_size),
+                      device)
+
+
+def _tile_pool(q, k, v, rows, vbs, nb, be):
+    b, h, s_out, d = q.shape
+    tiled = (b, h, nb * be, d)
+    qt, kt, vt = (torch.empty(tiled, device=q.device, dtype=q.dtype) for _ in range(3))
+    qc, kc, vc = (torch.empty((b, h, nb, d), device=q.device, dtype=q.dtype) for _ in range(3))
+    _lib.call("vsa_tile_pool_qkv", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(rows),
+              _lib.ptr(vbs), _lib.ptr(qt), _lib.ptr(kt), _lib.ptr(vt), _lib.ptr(qc),
+              _lib.ptr(kc), _lib.ptr(vc), b * h, s_out, nb, d, be, _lib.dtype_code(q.dtype),
+              _lib.stream_of(q))
+    return qt, kt, vt, qc, kc, vc
+
+
+def _forward(q, k, v, gate, rows, vbs, topk, nb, be, scale, want_lse):
+    b, h, s_out, d = q.shape
+    qt, kt, vt, qc, kc, vc = _tile_pool(q, k, v, rows, vbs, nb, be)
+    _, probs, outc, sel = M.coarse_forward(qc, kc, vc, topk, scale)
+    L = nb * be
+    out = torch.empty_like(q)
+    lse = torch.empty((b, h, L), device=q.device, dtype=torch.float32) if want_lse else None
+    fine = torch.empty_like(qt) if want_lse else None
+    gmode = M._gate_mode(gate, d, q.dtype)
+    _lib.call("vsa_sparse_fwd_tiled", _lib.ptr(qt), _lib.ptr(kt), _lib.ptr(vt), _lib.ptr(sel),
+              _lib.ptr(vbs), _lib.ptr(out), _lib.ptr(fine), _lib.ptr(lse), _lib.ptr(outc),
+              _lib.ptr(gate), gmode, _lib.ptr(rows), s_out, b * h, L, L, d, be, topk,
+              float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    return out, (qt, kt, vt, qc, kc, vc, probs, outc, sel, fine, lse)
+
+
+class _VSATiled(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, gate, rows, vbs, topk_, nb, be, scale):
+        out, saved = _forward(q, k, v, gate, rows, vbs, topk_, nb, be, scale, True)
+        ctx.save_for_backward(gate, rows, vbs, *saved)
+        ctx.dims = (q.shape, nb, be, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        gate, rows, vbs, qt, kt, vt, qc, kc, vc, probs, outc, sel, fine, lse = ctx.saved_tensors
+        (b, h, s_out, d), nb, be, scale = ctx.dims
+        L = nb * be
+        dout = dout.contiguous()
+        code, stream = _lib.dtype_code(dout.dtype), _lib.stream_of(dout)
+        delta = torch.empty((b, h, L), device=dout.device, dtype=torch.float32)
+        d_outc = torch.empty_like(outc)
+        d_gate = torch.empty_like(gate) if gate is not None else None
+        dout_t = torch.empty_like(qt)
+        gmode = M._gate_mode(gate, d, dout.dtype)
+        _lib.call("vsa_bwd_prep_tiled", _lib.ptr(fine), _lib.ptr(dout), _lib.ptr(outc),
+                  _lib.ptr(gate), gmode, _lib.ptr(rows), s_out, _lib.ptr(delta),
+                  _lib.ptr(d_outc), _lib.ptr(d_gate), _lib.ptr(dout_t), b * h, L, d, be, code,
+                  stream)
+        dqc, dkc, dvc = M.coarse_backward(qc, kc, vc, probs, d_outc, scale)
+        tk = sel.shape[-1]
+        dq = torch.empty((b, h, s_out, d), device=dout.device, dtype=dout.dtype)
+        dk, dv = torch.empty_like(dq), torch.empty_like(dq)
+        _lib.call("vsa_sparse_bwd_dq_tiled", _lib.ptr(qt), _lib.ptr(kt), _lib.ptr(vt),
+                  _lib.ptr(dout_t), _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(sel), _lib.ptr(vbs),
+                  _lib.ptr(dq), _lib.ptr(dqc), _lib.ptr(vbs), _lib.ptr(rows), s_out, b * h, L, L,
+                  d, be, tk, float(scale), code, stream)
+        inverse, offsets, counts = M.invert_routes(sel, nb)
+        order = M.dkdv_tile_order(counts, b * h, L, d, be)
+        _lib.call("vsa_sparse_bwd_dkdv_tiled", _lib.ptr(qt), _lib.ptr(kt), _lib.ptr(vt),
+                  _lib.ptr(dout_t), _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(counts),
+                  _lib.ptr(offsets), _lib.ptr(inverse), _lib.ptr(vbs), _lib.ptr(dk), _lib.ptr(dv),
+                  _lib.ptr(dkc), _lib.ptr(dvc), _lib.ptr(rows), s_out, b * h, L, L, d, be, tk,
+                  float(scale), _lib.ptr(order), code, stream)
+        return dq, dk, dv, d_gate, None, None, None, None, None, None
+
+
+def _composition(q, k, v, meta, nb, be, tile_size, topk, gate):
+    """untile(mi355x_vsa(tile(q), tile(k), tile(v), ...)) along the sequence dim."""
+    tpi, npi = meta["tile_partition_indices"], meta["non_pad_index"]
+    rev, vbs = meta["reverse_tile_partition_indices"], meta["variable_block_sizes"]
+
+    def tl(x):
+        return tiling.tile(x.transpose(1, 2), tpi, npi, nb, be).transpose(1, 2)
+
+    g = None
+    if gate is not None:
+        per_token = gate.shape[-1] == 1 and q.shape[-1] != 1
+        g = tl(torch.broadcast_to(gate, (*q.shape[:3], 1) if per_token else q.shape))
+    out = M.mi355x_vsa(tl(q), tl(k), tl(v), vbs, vbs, topk, tile_size, g)
+    return tiling.untile(out.transpose(1, 2), npi, rev).transpose(1, 2)
+
+
+def mi355x_vsa_tiled(q: Tensor, k: Tensor, v: Tensor, dit_seq_shape: Tuple[int, int, int],
+                     topk: int, tile_size: Tuple[int, int, int] = tiling.VSA_TILE_SIZE,
+                     compress_attn_weight: Optional[Tensor] = None) -> Tensor:
+    """VSA on raster-order tokens ``[B, H, T*H*W, D]`` of a ``(T, H, W)`` latent grid.
+
+    Equals ``untile(mi355x_vsa(tile(q), tile(k), tile(v), vbs, vbs, topk,
+    tile_size, tile(gate)))`` with tile / untile along the sequence dim and
+    ``vbs`` the tiles' real-token counts (build_vsa_metadata), bit for bit;
+    the tile and untile passes (fastvideo_tiling.py:130-145) are fused into
+    the op's own passes.  Returns raster-order ``[B, H, T*H*W, D]``."""
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("mi355x_vsa_tiled expects q, k, v of one shape [batch, heads, seq_len, "
+                         "head_dim] (self-attention over a raster-order video sequence)")
+    shape = tuple(int(x) for x in dit_seq_shape)
+    ts = tuple(int(x) for x in tile_size)
+    if len(shape) != 3 or len(ts) != 3 or min(shape) <= 0 or min(ts) <= 0:
+        raise ValueError("dit_seq_shape and tile_size must be three positive sizes (T, H, W)")
+    s_out = math.prod(shape)
+    if q.shape[2] != s_out:
+        raise ValueError(f"seq_len {q.shape[2]} is not T*H*W = {s_out} of dit_seq_shape {shape}")
+    if compress_attn_weight is not None:
+        try:
+            ok = torch.broadcast_shapes(compress_attn_weight.shape, q.shape) == q.shape
+        except RuntimeError:
+            ok = False
+        if not ok:
+            raise ValueError("compress_attn_weight must have the same shape as q, or a shape "
+                             "that broadcasts to it (e.g. [batch, heads, seq_len, 1])")
+    be = math.prod(ts)
+    nb = math.ceil(shape[0] / ts[0]) * math.ceil(shape[1] / ts[1]) * math.ceil(shape[2] / ts[2])
+    M._check_device_path(q, k, v, be)
+    gate = compress_attn_weight
+    b, h, _, d = q.shape
+    fused_gate = gate is None or (gate.dtype == q.dtype and gate.device == q.device and
+                                  tuple(gate.shape) in ((b, h, s_out, d), (b, h, s_out, 1)))
+    fused = (q.dtype in M.MFMA_DTYPES and d in FUSED_HEAD_DIMS and be in FUSED_BLOCKS
+             and fused_gate and 1 <= topk <= nb)
+    with torch.cuda.device(q.device):
+        meta = tiling.build_vsa_metadata(shape, ts, device=q.device)
+        if not fused:
+            return _composition(q, k, v, meta, nb, be, ts, topk, gate)
+        vbs = meta["variable_block_sizes"].to(torch.int32)
+        rows = slot_rows(shape, ts, q.device)
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        if gate is not None:
+            gate = gate.contiguous()
+        scale = 1.0 / math.sqrt(d)
+        needs_grad = torch.is_grad_enabled() and (
+            q.requires_grad or k.requires_grad or v.requires_grad
+            or (gate is not None and gate.requires_grad))
+        if needs_grad:
+            return _VSATiled.apply(q, k, v, gate, rows, vbs, topk, nb, be, scale)
+        return _forward(q, k, v, gate, rows, vbs, topk, nb, be, scale, False)[0]

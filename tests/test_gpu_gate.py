@@ -158,3 +158,23 @@ def test_gate_that_does_not_broadcast_is_rejected():
     vbs = torch.full((2,), 256, device=DEV, dtype=torch.int32)
     with pytest.raises(ValueError, match="compress_attn_weight"):
         M.mi355x_vsa(q, q, q, vbs, vbs, 1, (4, 8, 8), torch.rand(1, 2, 512, 32, device=DEV))
+
+
+@pytest.mark.parametrize("heads", [3, 22])
+def test_per_token_gate_as_a_transposed_view_is_read_by_its_values(heads):
+    """A [B, H, S, 1] gate that is the transpose of a contiguous [B, S, H, 1]
+    tensor has the strides of a token-major full gate; it must still be read
+    as the per-token gate it is (regression: it used to be passed through
+    uncopied and read as if contiguous)."""
+    from vsa_mi355x import mi355x as M
+    g = torch.Generator(device=DEV).manual_seed(87 + heads)
+    q, k, v = (torch.randn(1, heads, 1024, 128, generator=g, device=DEV, dtype=torch.bfloat16)
+               for _ in range(3))
+    base = 2.0 * torch.rand(1, 1024, heads, 1, generator=g, device=DEV, dtype=torch.bfloat16)
+    view = base.transpose(1, 2)
+    assert not view.is_contiguous()
+    vbs = torch.full((4,), 256, device=DEV, dtype=torch.int32)
+    with torch.no_grad():
+        a = M.mi355x_vsa(q, k, v, vbs, vbs, 2, (4, 8, 8), view)
+        b = M.mi355x_vsa(q, k, v, vbs, vbs, 2, (4, 8, 8), view.contiguous())
+    assert torch.equal(a, b)

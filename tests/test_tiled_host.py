@@ -1,0 +1,40 @@
+"""Host-side checks of mi355x_vsa_tiled (no GPU needed): argument validation
+runs before any device work, and CPU tensors are rejected, never computed on
+the host."""
+
+import pytest
+import torch
+
+from vsa_mi355x import tiled
+
+
+def _qkv(s, d=64):
+    return [torch.zeros(1, 2, s, d) for _ in range(3)]
+
+
+def test_sequence_length_must_be_the_latent_volume():
+    with pytest.raises(ValueError, match=r"is not T\*H\*W"):
+        tiled.mi355x_vsa_tiled(*_qkv(100), (4, 5, 6), 2)
+
+
+def test_q_k_v_must_share_one_shape():
+    q, k, v = _qkv(120)
+    with pytest.raises(ValueError, match="one shape"):
+        tiled.mi355x_vsa_tiled(q, k[:, :, :60], v, (4, 5, 6), 2)
+
+
+def test_shape_and_tile_must_be_three_positive_sizes():
+    with pytest.raises(ValueError, match="three positive sizes"):
+        tiled.mi355x_vsa_tiled(*_qkv(120), (4, 5, 6), 2, (4, 4))
+    with pytest.raises(ValueError, match="three positive sizes"):
+        tiled.mi355x_vsa_tiled(*_qkv(120), (4, 5, 6), 2, (4, 0, 4))
+
+
+def test_gate_must_broadcast_to_q():
+    with pytest.raises(ValueError, match="compress_attn_weight"):
+        tiled.mi355x_vsa_tiled(*_qkv(120), (4, 5, 6), 2, (4, 4, 4), torch.zeros(1, 2, 7, 1))
+
+
+def test_cpu_tensors_are_rejected():
+    with pytest.raises(ValueError, match="requires GPU tensors"):
+        tiled.mi355x_vsa_tiled(*_qkv(120), (4, 5, 6), 2, (4, 4, 4))
