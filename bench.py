@@ -284,6 +284,43 @@ def run_gate(steps, warmup):
     return res
 
 
+def run_tiled(steps, warmup):
+    """c3 as a video DiT holds it: raster-order tokens of a 20x32x64 latent in
+    (4,8,8) tiles (40,960 tokens, 160 blocks of 256), gate [B,H,S,D].  fwd+bwd
+    of mi355x_vsa_tiled (tile / untile fused into the op) against the unfused
+    tile -> mi355x_vsa -> untile composition."""
+    import torch
+    from vsa_mi355x import tiled, tiling
+    B, H, D, topk = CFG["B"], CFG["H"], CFG["D"], CFG["topk"]
+    shape, ts = (20, 32, 64), CFG["block"]
+    S = math.prod(shape)
+    nb, be = math.prod([math.ceil(a / b) for a, b in zip(shape, ts)]), math.prod(ts)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+                   for _ in range(4))
+    gate = torch.rand(B, H, S, D, generator=g, device=dev, dtype=torch.bfloat16)
+    leaves = [t.requires_grad_() for t in (q, k, v, gate)]
+    meta = tiling.build_vsa_metadata(shape, ts, device=dev)
+    res = {"workload": "tiled", "latent": list(shape), "tile": list(ts)}
+    runs = (("fused", lambda: tiled.mi355x_vsa_tiled(q, k, v, shape, topk, ts, gate)),
+            ("composition", lambda: tiled._composition(q, k, v, meta, nb, be, ts, topk, gate)))
+    for name, fwd in runs:
+        def step():
+            torch.autograd.grad(fwd(), leaves, do)
+
+        def fwd_only():
+            with torch.no_grad():
+                fwd()
+        for _ in range(warmup):
+            step()
+        res[name + "_fwd_bwd_ms"] = round(_events_time(step, steps), 3)
+        res[name + "_fwd_ms"] = round(_events_time(fwd_only, steps), 3)
+    res["saved_fwd_bwd_ms"] = round(res["composition_fwd_bwd_ms"] - res["fused_fwd_bwd_ms"], 3)
+    res["saved_fwd_ms"] = round(res["composition_fwd_ms"] - res["fused_fwd_ms"], 3)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,7 +335,8 @@ def main():
                          "reported under 'workloads' of the c3 line; 0 skips them")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of the workload timed on the CPU oracle (one at a time)")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["tiling", "gate"], default="c3",
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["tiling", "gate", "tiled"],
+                    default="c3",
                     help="BASELINE configuration to run (c3 is the metric's workload)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -325,6 +363,9 @@ def main():
         return
     if args.workload == "tiling":
         print(json.dumps(run_tiling(args.steps, args.warmup)), flush=True)
+        return
+    if args.workload == "tiled":
+        print(json.dumps(run_tiled(args.steps, args.warmup)), flush=True)
         return
     if args.workload != "c3":
         print(json.dumps(run_workload(args.workload, args.steps, args.warmup)), flush=True)

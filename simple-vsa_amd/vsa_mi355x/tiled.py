@@ -132,19 +132,22 @@ class _VSATiled(torch.autograd.Function):
 
 
 def _composition(q, k, v, meta, nb, be, tile_size, topk, gate):
-    """untile(mi355x_vsa(tile(q), tile(k), tile(v), ...)) along the sequence dim."""
+    """untile(mi355x_vsa(tile(q), tile(k), tile(v), ...)) along the sequence dim
+    (batch and heads folded into tile's batch dim, so no transposes)."""
     tpi, npi = meta["tile_partition_indices"], meta["non_pad_index"]
     rev, vbs = meta["reverse_tile_partition_indices"], meta["variable_block_sizes"]
 
     def tl(x):
-        return tiling.tile(x.transpose(1, 2), tpi, npi, nb, be).transpose(1, 2)
+        b, h, s, c = x.shape
+        return tiling.tile(x.reshape(b * h, s, c), tpi, npi, nb, be).view(b, h, nb * be, c)
 
     g = None
     if gate is not None:
         per_token = gate.shape[-1] == 1 and q.shape[-1] != 1
         g = tl(torch.broadcast_to(gate, (*q.shape[:3], 1) if per_token else q.shape))
     out = M.mi355x_vsa(tl(q), tl(k), tl(v), vbs, vbs, topk, tile_size, g)
-    return tiling.untile(out.transpose(1, 2), npi, rev).transpose(1, 2)
+    b, h, _, d = out.shape
+    return tiling.untile(out.reshape(b * h, nb * be, d), npi, rev).view(b, h, -1, d)
 
 
 def mi355x_vsa_tiled(q: Tensor, k: Tensor, v: Tensor, dit_seq_shape: Tuple[int, int, int],
