@@ -285,7 +285,9 @@ __device__ __forceinline__ void dkdv_tile(
   const int64_t b = tile / tiles_per_head;
   const int k0 = (tile % tiles_per_head) * C::KT;  // first key (within head)
   const int kvblk = k0 / BE;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // the wave index is uniform: every direct-load LDS base derived from it stays
+  // on the scalar unit (no per-copy read-back of a vector register)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, h = lane >> 5;
   const int mykey = k0 + wave * 32 + r;
   const int64_t ktok = (int64_t)b * skv + mykey;
