@@ -113,3 +113,28 @@ def test_unfused_shapes_run_the_composition():
     meta = tiling.build_vsa_metadata(shape, ts, device=DEV)
     ref = tiled._composition(qd, kd, vd, meta, 4, 64, ts, 2, gate)
     assert torch.equal(out, ref)
+
+
+def test_fused_tiled_op_at_c3_size_equals_the_composition():
+    """The c3 workload as a video DiT holds it: a 20x32x64 latent in (4,8,8)
+    tiles, 40 heads, head_dim 128, topk 20, full gate; output and every
+    gradient bit for bit (the ping-pong forward / dQ and the persistent dK/dV
+    at their real grid sizes)."""
+    from vsa_mi355x import tiled, tiling
+    shape, ts, H, d, tk = (20, 32, 64), (4, 8, 8), 40, 128, 20
+    g = torch.Generator(device=DEV).manual_seed(91)
+    s = math.prod(shape)
+    q, k, v, do = (torch.randn(1, H, s, d, generator=g, device=DEV, dtype=torch.bfloat16)
+                   for _ in range(4))
+    gate = torch.rand(1, H, s, d, generator=g, device=DEV, dtype=torch.bfloat16)
+    meta = tiling.build_vsa_metadata(shape, ts, device=DEV)
+    outs = []
+    for fn in (lambda *a: tiled.mi355x_vsa_tiled(*a[:3], shape, tk, ts, a[3]),
+               lambda *a: tiled._composition(*a[:3], meta, 160, 256, ts, tk, a[3])):
+        leaves = [x.clone().requires_grad_() for x in (q, k, v, gate)]
+        out = fn(*leaves)
+        grads = torch.autograd.grad(out, leaves, do)
+        outs.append([out.detach()] + list(grads))
+        del out, grads, leaves
+    for name, a, b in zip(["out", "dq", "dk", "dv", "dgate"], *outs):
+        assert torch.equal(a, b), (name, (a.float() - b.float()).abs().max().item())
