@@ -286,9 +286,10 @@ def run_gate(steps, warmup):
 
 def run_tiled(steps, warmup):
     """c3 as a video DiT holds it: raster-order tokens of a 20x32x64 latent in
-    (4,8,8) tiles (40,960 tokens, 160 blocks of 256), gate [B,H,S,D].  fwd+bwd
-    of mi355x_vsa_tiled (tile / untile fused into the op) against the unfused
-    tile -> mi355x_vsa -> untile composition."""
+    (4,8,8) tiles (40,960 tokens, 160 blocks of 256), gate of q's shape.
+    fwd+bwd of mi355x_vsa_tiled (tile / untile fused into the op) against the
+    unfused tile -> mi355x_vsa -> untile composition, with q, k, v, gate, dout
+    head-major [B, H, S, D] and token-major [B, S, H, D]."""
     import torch
     from vsa_mi355x import tiled, tiling
     B, H, D, topk = CFG["B"], CFG["H"], CFG["D"], CFG["topk"]
@@ -303,21 +304,35 @@ def run_tiled(steps, warmup):
     leaves = [t.requires_grad_() for t in (q, k, v, gate)]
     meta = tiling.build_vsa_metadata(shape, ts, device=dev)
     res = {"workload": "tiled", "latent": list(shape), "tile": list(ts)}
-    runs = (("fused", lambda: tiled.mi355x_vsa_tiled(q, k, v, shape, topk, ts, gate)),
-            ("composition", lambda: tiled._composition(q, k, v, meta, nb, be, ts, topk, gate)))
-    for name, fwd in runs:
-        def step():
-            torch.autograd.grad(fwd(), leaves, do)
+    # token-major [B, S, H, D] copies: the layout a DiT's projections produce
+    qt, kt, vt, gt = (x.detach().transpose(1, 2).contiguous().requires_grad_()
+                      for x in (q, k, v, gate))
+    dot = do.transpose(1, 2).contiguous()
+    runs = (("fused", lambda: tiled.mi355x_vsa_tiled(q, k, v, shape, topk, ts, gate), leaves, do),
+            ("composition", lambda: tiled._composition(q, k, v, meta, nb, be, ts, topk, gate),
+             leaves, do),
+            ("token_major_fused", lambda: tiled.mi355x_vsa_tiled(qt, kt, vt, shape, topk, ts, gt,
+                                                                 token_major=True),
+             [qt, kt, vt, gt], dot),
+            ("token_major_composition", lambda: tiled._composition(qt, kt, vt, meta, nb, be, ts,
+                                                                   topk, gt, token_major=True),
+             [qt, kt, vt, gt], dot))
+    for name, fwd, lv, grad in runs:
+        def step(fwd=fwd, lv=lv, grad=grad):
+            torch.autograd.grad(fwd(), lv, grad)
 
-        def fwd_only():
+        def fwd_only(fwd=fwd):
             with torch.no_grad():
                 fwd()
         for _ in range(warmup):
             step()
         res[name + "_fwd_bwd_ms"] = round(_events_time(step, steps), 3)
         res[name + "_fwd_ms"] = round(_events_time(fwd_only, steps), 3)
-    res["saved_fwd_bwd_ms"] = round(res["composition_fwd_bwd_ms"] - res["fused_fwd_bwd_ms"], 3)
-    res["saved_fwd_ms"] = round(res["composition_fwd_ms"] - res["fused_fwd_ms"], 3)
+    for pre in ("", "token_major_"):
+        res[pre + "saved_fwd_bwd_ms"] = round(res[pre + "composition_fwd_bwd_ms"]
+                                              - res[pre + "fused_fwd_bwd_ms"], 3)
+        res[pre + "saved_fwd_ms"] = round(res[pre + "composition_fwd_ms"]
+                                          - res[pre + "fused_fwd_ms"], 3)
     return res
 
 

@@ -300,7 +300,11 @@ int vsa_rows_zero_unmarked(void* out, int64_t out_rows, int64_t batch, int64_t r
  * value equals the unfused composition tile -> op -> untile bit for bit.
  * slot_rows[nb*be] (int32) maps a tiled slot n*be + p to its raster token,
  * -1 for a padding slot; it is shared by every batch and head.  s_out is the
- * raster length T*H*W, sq = skv = nb*be the tiled length.  bf16 / fp16, head
+ * raster length T*H*W, sq = skv = nb*be the tiled length.  The raster tensors
+ * are head-major [bh, s_out, D] when heads == 0, or token-major
+ * [bh / heads, s_out, heads, D] (a projection's [B, S, H, D] output, tile()'s
+ * own [batch, seq, ...] layout) when heads > 0; the tiled tensors are always
+ * [bh, sq, D].  bf16 / fp16, head
  * dims 64 and 128, tiles of 64, 128 or 256 tokens; gate_mode 0, 1 or 2 in the
  * input dtype (callers fall back to the composition otherwise).
  */
@@ -322,8 +326,9 @@ int vsa_tile_slot_rows(int32_t T, int32_t H, int32_t W, int32_t ts, int32_t hs, 
  */
 int vsa_tile_pool_qkv(const void* q, const void* k, const void* v, const int32_t* slot_rows,
                       const int32_t* variable_block_sizes, void* q_t, void* k_t, void* v_t,
-                      void* q_c, void* k_c, void* v_c, int64_t bh, int64_t s_out, int32_t nb,
-                      int32_t head_dim, int32_t block_elements, int32_t dtype, void* stream);
+                      void* q_c, void* k_c, void* v_c, int64_t bh, int64_t s_out, int32_t heads,
+                      int32_t nb, int32_t head_dim, int32_t block_elements, int32_t dtype,
+                      void* stream);
 
 /*
  * vsa_sparse_fwd on tiled q, k, v with out (and a gate_mode 1 / 2 gate) in
@@ -333,9 +338,9 @@ int vsa_tile_pool_qkv(const void* q, const void* k, const void* v, const int32_t
 int vsa_sparse_fwd_tiled(const void* q, const void* k, const void* v, const int32_t* selected,
                          const int32_t* kv_variable_block_sizes, void* out, void* fine_out,
                          float* lse, const void* out_c, const void* gate, int32_t gate_mode,
-                         const int32_t* slot_rows, int64_t s_out, int64_t bh, int64_t sq,
-                         int64_t skv, int32_t head_dim, int32_t block_elements, int32_t topk,
-                         float scale, int32_t dtype, void* stream);
+                         const int32_t* slot_rows, int64_t s_out, int32_t heads, int64_t bh,
+                         int64_t sq, int64_t skv, int32_t head_dim, int32_t block_elements,
+                         int32_t topk, float scale, int32_t dtype, void* stream);
 
 /*
  * vsa_bwd_prep with dout and the gate in raster order and d_gate written in
@@ -345,9 +350,9 @@ int vsa_sparse_fwd_tiled(const void* q, const void* k, const void* v, const int3
  */
 int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const void* out_c,
                        const void* gate, int32_t gate_mode, const int32_t* slot_rows,
-                       int64_t s_out, float* delta, void* d_out_c, void* d_gate, void* dout_t,
-                       int64_t bh, int64_t sq, int32_t head_dim, int32_t block_elements,
-                       int32_t dtype, void* stream);
+                       int64_t s_out, int32_t heads, float* delta, void* d_out_c, void* d_gate,
+                       void* dout_t, int64_t bh, int64_t sq, int32_t head_dim,
+                       int32_t block_elements, int32_t dtype, void* stream);
 
 /*
  * vsa_sparse_bwd_dq on tiled inputs (dout = dout_t) with dq written in raster
@@ -358,7 +363,7 @@ int vsa_sparse_bwd_dq_tiled(const void* q, const void* k, const void* v, const v
                             const float* lse, const float* delta, const int32_t* selected,
                             const int32_t* kv_variable_block_sizes, void* dq, const void* d_q_c,
                             const int32_t* q_variable_block_sizes, const int32_t* slot_rows,
-                            int64_t s_out, int64_t bh, int64_t sq, int64_t skv,
+                            int64_t s_out, int32_t heads, int64_t bh, int64_t sq, int64_t skv,
                             int32_t head_dim, int32_t block_elements, int32_t topk, float scale,
                             int32_t dtype, void* stream);
 
@@ -371,7 +376,7 @@ int vsa_sparse_bwd_dkdv_tiled(const void* q, const void* k, const void* v, const
                               const int32_t* offsets, const int32_t* inverse,
                               const int32_t* kv_variable_block_sizes, void* dk, void* dv,
                               const void* d_k_c, const void* d_v_c, const int32_t* slot_rows,
-                              int64_t s_out, int64_t bh, int64_t sq, int64_t skv,
+                              int64_t s_out, int32_t heads, int64_t bh, int64_t sq, int64_t skv,
                               int32_t head_dim, int32_t block_elements, int32_t topk, float scale,
                               int32_t* tile_order, int32_t dtype, void* stream);
 

@@ -78,7 +78,8 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(
 
 // ---------------------------------------------------------------------------
 // tile() and the padded block mean in one pass: x (q, k or v) is a
-// raster-order sequence of s_out tokens per head; the tiled copy xt gets row
+// raster-order sequence of s_out tokens per head (head-major, or token-major
+// [B, s_out, heads, D] when heads > 0); the tiled copy xt gets row
 // t of block n from raster row rows[n*be + t] (zero at a padding slot, < 0),
 // and the block mean sums the valid rows of that copy in the order
 // pool_qkv_kernel does, so both equal tile() followed by the pooling pass.
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(256) void tile_pool_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ rows, const int32_t* __restrict__ vbs, T* __restrict__ qt,
     T* __restrict__ kt, T* __restrict__ vt, T* __restrict__ qc, T* __restrict__ kc,
-    T* __restrict__ vc, int64_t bh, int nb, int D, int be, int64_t s_out) {
+    T* __restrict__ vc, int64_t bh, int nb, int D, int be, int64_t s_out, int heads) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float part[256 * VEC];
   int64_t id = blockIdx.x;
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256) void tile_pool_kernel(
   const int32_t cnt = vbs[n];
   const int valid = clamp_valid(cnt, be);
   const float div = (float)(cnt > 1 ? cnt : 1);
-  const T* src = x + head * s_out * D;
+
   T* dst = xt + id * (int64_t)be * D;
   const int32_t* brows = rows + (int64_t)n * be;
   const int tpr = D / VEC, rpi = 256 / tpr;
@@ -125,7 +126,8 @@ __global__ __launch_bounds__(256) void tile_pool_kernel(
       if (t < be) {
         const int r = brows[t];
         if (r >= 0 && r < s_out)
-          raw[u] = ld_stream(reinterpret_cast<const u32x4*>(src + (int64_t)r * D + col * VEC));
+          raw[u] = ld_stream(reinterpret_cast<const u32x4*>(
+              x + raster_row(head, r, s_out, heads) * D + col * VEC));
       }
     }
 #pragma unroll
@@ -325,7 +327,7 @@ __device__ __forceinline__ void store_gate(G* __restrict__ p, const float* v) {
 // gradient is then stored in fp32, as the reference stores it in the gate's
 // dtype, fused_common.py:202-221).
 // With RASTER, dout, the gate and d_gate are raster-order sequences of s_out
-// tokens: tiled slot n*be + t of a head is raster row rows[n*be + t] (< 0 for a
+// tokens (head-major, or token-major [B, s_out, heads, ...] when heads > 0): tiled slot n*be + t of a head is raster row rows[n*be + t] (< 0 for a
 // padding slot, whose dout and gate read as zero and which has no d_gate
 // row), and the pass also writes dout in the tiled layout (dout_t, zero rows
 // at the padding slots) for the fine backward kernels.  Every value is then
@@ -336,7 +338,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     const T* __restrict__ fine, const T* __restrict__ dout, const T* __restrict__ outc,
     const G* __restrict__ gate, int gate_mode, int gate_heads, float* __restrict__ delta,
     T* __restrict__ d_outc, G* __restrict__ d_gate, int qb, int D, int be,
-    const int32_t* __restrict__ rows = nullptr, int64_t s_out = 0, T* __restrict__ dout_t = nullptr) {
+    const int32_t* __restrict__ rows = nullptr, int64_t s_out = 0, int heads = 0,
+    T* __restrict__ dout_t = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float part[256 * VEC];
   const int64_t blk = blockIdx.x + (int64_t)blockIdx.y * qb;  // bh*qb + n
@@ -372,7 +375,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       ro[u] = ld_stream(reinterpret_cast<const u32x4*>(fine + off));
       if constexpr (RASTER) {
         const int r = rows[(int64_t)blockIdx.x * be + t];
-        rtok[u] = (r >= 0 && r < s_out) ? bh * s_out + r : -1;
+        rtok[u] = (r >= 0 && r < s_out) ? raster_row(bh, r, s_out, heads) : -1;
         const bool real = rtok[u] >= 0;
         rd[u] = real ? ld_stream(reinterpret_cast<const u32x4*>(dout + rtok[u] * D + c0))
                      : u32x4{0u, 0u, 0u, 0u};
@@ -636,10 +639,11 @@ extern "C" int vsa_pool_qkv(const void* q, const void* k, const void* v, const i
 extern "C" int vsa_tile_pool_qkv(const void* q, const void* k, const void* v,
                                  const int32_t* slot_rows, const int32_t* vbs, void* q_t,
                                  void* k_t, void* v_t, void* q_c, void* k_c, void* v_c,
-                                 int64_t bh, int64_t s_out, int32_t nb, int32_t D, int32_t be,
-                                 int32_t dtype, void* stream) {
+                                 int64_t bh, int64_t s_out, int32_t heads, int32_t nb, int32_t D,
+                                 int32_t be, int32_t dtype, void* stream) {
   if (!q || !k || !v || !slot_rows || !vbs || !q_t || !k_t || !v_t || !q_c || !k_c || !v_c)
     return VSA_ERR_NULL;
+  if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (bh <= 0 || nb <= 0 || be <= 0 || be > 256 || s_out <= 0 || s_out > (int64_t)nb * be ||
       !vec_dim_ok(D, dtype))
     return VSA_ERR_SHAPE;
@@ -649,7 +653,7 @@ extern "C" int vsa_tile_pool_qkv(const void* q, const void* k, const void* v,
   VSA_DISPATCH_ALL(dtype, T, {
     hipLaunchKernelGGL(tile_pool_kernel<T>, dim3((unsigned)grid), dim3(256), 0, s, (const T*)q,
                        (const T*)k, (const T*)v, slot_rows, vbs, (T*)q_t, (T*)k_t, (T*)v_t,
-                       (T*)q_c, (T*)k_c, (T*)v_c, bh, nb, D, be, s_out);
+                       (T*)q_c, (T*)k_c, (T*)v_c, bh, nb, D, be, s_out, heads);
   });
   return vsa_check_launch();
 }
@@ -738,10 +742,11 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
 
 extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const void* out_c,
                                   const void* gate, int32_t gate_mode, const int32_t* slot_rows,
-                                  int64_t s_out, float* delta, void* d_out_c, void* d_gate,
-                                  void* dout_t, int64_t bh, int64_t sq, int32_t D, int32_t be,
-                                  int32_t dtype, void* stream) {
+                                  int64_t s_out, int32_t heads, float* delta, void* d_out_c,
+                                  void* d_gate, void* dout_t, int64_t bh, int64_t sq, int32_t D,
+                                  int32_t be, int32_t dtype, void* stream) {
   if (!fine_out || !dout || !delta || !slot_rows || !dout_t) return VSA_ERR_NULL;
+  if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;  // no token-major / fp32 gate here
   if (out_c && !d_out_c) return VSA_ERR_NULL;
   if (out_c && gate_mode != 0 && (!gate || !d_gate)) return VSA_ERR_NULL;
@@ -755,7 +760,7 @@ extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const 
     hipLaunchKernelGGL((bwd_prep_kernel<T, T, true>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
                        (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate,
                        gate_mode, 1, delta, (T*)d_out_c, (T*)d_gate, qb, D, be, slot_rows, s_out,
-                       (T*)dout_t);
+                       heads, (T*)dout_t);
   });
   return vsa_check_launch();
 }

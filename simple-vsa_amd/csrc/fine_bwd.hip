@@ -48,13 +48,13 @@ __device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64
                                             const T* __restrict__ dqc,
                                             const int32_t* __restrict__ q_vbs, float scale,
                                             const int32_t* __restrict__ orows = nullptr,
-                                            int64_t s_out = 0) {
+                                            int64_t s_out = 0, int heads = 0) {
   using E = Elem<T>;
   int64_t tok = (int64_t)b * sq + myq;
   if constexpr (RASTER) {
     const int r = orows[myq];
     if (r < 0 || r >= s_out) return;
-    tok = (int64_t)b * s_out + r;
+    tok = raster_row(b, r, s_out, heads);
   }
   const int qpos = myq - qblk * BE;
   float cdiv = 1.f;
@@ -105,7 +105,7 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
                  const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
                  const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
                  int tiles_per_head, int sq, int skv, int qb, int kb, int topk, float c2,
-                 uint32_t qsign, float scale, const int32_t* __restrict__ orows, int64_t s_out) {
+                 uint32_t qsign, float scale, const int32_t* __restrict__ orows, int64_t s_out, int heads) {
   using C = DqCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
@@ -211,7 +211,7 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   }
 
   dq_epilogue<T, D, BE, RASTER>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale, orows,
-                                s_out);
+                                s_out, heads);
 }
 
 // ===========================================================================
@@ -271,7 +271,7 @@ __device__ __forceinline__ void dkdv_tile(
     T* __restrict__ dk, T* __restrict__ dv, const T* __restrict__ dkc,
     const T* __restrict__ dvc, int tiles_per_head, int sq, int skv, int qb,
     int kb, int topk, float c2, uint32_t ksign, float scale,
-    const int32_t* __restrict__ orows, int64_t s_out) {
+    const int32_t* __restrict__ orows, int64_t s_out, int heads) {
   using C = DkvCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
@@ -564,7 +564,7 @@ epilogue:
   int64_t otok = ktok;
   if constexpr (RASTER) {
     const int r = orows[mykey];
-    otok = (r >= 0 && r < s_out) ? (int64_t)b * s_out + r : -1;
+    otok = (r >= 0 && r < s_out) ? raster_row(b, r, s_out, heads) : -1;
   }
   const bool ostore = !RASTER || otok >= 0;
   const float cdiv = (float)(cnt > 1 ? cnt : 1), rcp = 1.0f / cdiv;
@@ -635,7 +635,7 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     T* __restrict__ dk, T* __restrict__ dv, const T* __restrict__ dkc,
     const T* __restrict__ dvc, int num_tiles, int tiles_per_head, int sq, int skv, int qb,
     int kb, int topk, float c2, uint32_t ksign, float scale, int32_t* __restrict__ tile_order,
-    const int32_t* __restrict__ orows, int64_t s_out) {
+    const int32_t* __restrict__ orows, int64_t s_out, int heads) {
   __shared__ DkvShared<T, D, BE> sh;
   if constexpr (DkvCfg<D, BE>::NSPLIT > 1) {
     // head_dim 256: one tile per workgroup (the loop's state would push the
@@ -644,7 +644,7 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     if (tile_s < num_tiles)
       dkdv_tile<T, D, BE, RASTER>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets,
                                   inverse, kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb,
-                                  kb, topk, c2, ksign, scale, orows, s_out);
+                                  kb, topk, c2, ksign, scale, orows, s_out, heads);
     return;
   }
   __shared__ int s_next;
@@ -666,7 +666,7 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     if (tile_s < num_tiles)
       dkdv_tile<T, D, BE, RASTER>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets,
                                   inverse, kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb,
-                                  kb, topk, c2, ksign, scale, orows, s_out);
+                                  kb, topk, c2, ksign, scale, orows, s_out, heads);
     dma_wait();       // this wave's trailing copies land before the LDS is reused
     __syncthreads();  // and every wave is done with it (and with s_next)
   }
@@ -707,7 +707,7 @@ __device__ __forceinline__ void dq_pp_tile(
     const float* __restrict__ delta, const int32_t* __restrict__ selected,
     const int32_t* __restrict__ kv_vbs, T* __restrict__ dq, const T* __restrict__ dqc,
     const int32_t* __restrict__ q_vbs, int sq, int skv, int qb, int kb, int topk, float c2,
-    uint32_t qsign, float scale, const int32_t* __restrict__ orows, int64_t s_out) {
+    uint32_t qsign, float scale, const int32_t* __restrict__ orows, int64_t s_out, int heads) {
   constexpr int BE = 256;
   using C = DqPPCfg<D>;
   using E = Elem<T>;
@@ -947,7 +947,7 @@ __device__ __forceinline__ void dq_pp_tile(
   }
   if (!grp1) phase_barrier();
   dq_epilogue<T, D, BE, RASTER>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale, orows,
-                                s_out);
+                                s_out, heads);
 }
 
 // Persistent, with the query-block walk of sparse_fwd_pp_kernel.
@@ -959,7 +959,7 @@ sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
                     const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
                     const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
-                    float scale, const int32_t* __restrict__ orows, int64_t s_out) {
+                    float scale, const int32_t* __restrict__ orows, int64_t s_out, int heads) {
   using C = DqPPCfg<D>;
   __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
   const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
@@ -967,7 +967,7 @@ sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
     const int tile = xcd * per + j;
     if (tile >= num_tiles) break;
     dq_pp_tile<T, D, RASTER>(smem, tile, q, k, v, dout, lse, delta, selected, kv_vbs, dq, dqc,
-                             q_vbs, sq, skv, qb, kb, topk, c2, qsign, scale, orows, s_out);
+                             q_vbs, sq, skv, qb, kb, topk, c2, qsign, scale, orows, s_out, heads);
     dma_wait();
     __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
   }
@@ -978,7 +978,7 @@ static int launch_dq_pp(const void* q, const void* k, const void* v, const void*
                         const float* lse, const float* delta, const int32_t* selected,
                         const int32_t* kv_vbs, void* dq, const void* dqc, const int32_t* q_vbs,
                         int64_t bh, int64_t sq, int64_t skv, int topk, float scale,
-                        hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0) {
+                        hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0, int heads = 0) {
   const int64_t tiles = bh * (sq / 256);
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   const int64_t want = ((tiles + 7) / 8) * 8;
@@ -988,7 +988,7 @@ static int launch_dq_pp(const void* q, const void* k, const void* v, const void*
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, selected,
                      kv_vbs, (T*)dq, (const T*)dqc, q_vbs, (int)tiles, (int)sq, (int)skv,
                      (int)(sq / 256), (int)(skv / 256), topk, fabsf(scale) * kLog2e,
-                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out);
+                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out, heads);
   return vsa_check_launch();
 }
 
@@ -997,7 +997,7 @@ static int launch_dq(const void* q, const void* k, const void* v, const void* do
                      const float* lse, const float* delta, const int32_t* selected,
                      const int32_t* kv_vbs, void* dq, const void* dqc, const int32_t* q_vbs,
                      int64_t bh, int64_t sq, int64_t skv, int topk, float scale,
-                     hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0) {
+                     hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0, int heads = 0) {
   using C = DqCfg<D, BE>;
   const int tph = (int)(sq / C::QT);
   const int64_t tiles = bh * tph;
@@ -1007,7 +1007,7 @@ static int launch_dq(const void* q, const void* k, const void* v, const void* do
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, selected,
                      kv_vbs, (T*)dq, (const T*)dqc, q_vbs, (int)tiles, tph, (int)sq, (int)skv,
                      (int)(sq / BE), (int)(skv / BE), topk, fabsf(scale) * kLog2e,
-                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out);
+                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out, heads);
   return vsa_check_launch();
 }
 
@@ -1017,7 +1017,7 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
                        const int32_t* offsets, const int32_t* inverse, const int32_t* kv_vbs,
                        void* dk, void* dv, const void* dkc, const void* dvc, int64_t bh,
                        int64_t sq, int64_t skv, int topk, float scale, int32_t* tile_order,
-                       hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0) {
+                       hipStream_t stream, const int32_t* orows = nullptr, int64_t s_out = 0, int heads = 0) {
   using C = DkvCfg<D, BE>;
   const int tph = (int)(skv / C::KT);
   const int64_t tiles = bh * tph * C::NSPLIT;
@@ -1032,7 +1032,7 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
                      offsets, inverse, kv_vbs, (T*)dk, (T*)dv, (const T*)dkc, (const T*)dvc,
                      (int)tiles, tph, (int)sq, (int)skv, (int)(sq / BE), (int)(skv / BE), topk,
                      fabsf(scale) * kLog2e, scale < 0.f ? 0x80008000u : 0u, scale, tile_order,
-                     orows, s_out);
+                     orows, s_out, heads);
   return vsa_check_launch();
 }
 
@@ -1305,7 +1305,7 @@ extern "C" int vsa_sparse_bwd_dq_tiled(const void* q, const void* k, const void*
                                        const void* dout, const float* lse, const float* delta,
                                        const int32_t* selected, const int32_t* kv_vbs, void* dq,
                                        const void* d_q_c, const int32_t* q_vbs,
-                                       const int32_t* slot_rows, int64_t s_out, int64_t bh,
+                                       const int32_t* slot_rows, int64_t s_out, int32_t heads, int64_t bh,
                                        int64_t sq, int64_t skv, int32_t D, int32_t be,
                                        int32_t topk, float scale, int32_t dtype, void* stream) {
   if (!q || !k || !v || !dout || !lse || !delta || !selected || !kv_vbs || !dq || !slot_rows)
@@ -1314,15 +1314,16 @@ extern "C" int vsa_sparse_bwd_dq_tiled(const void* q, const void* k, const void*
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       s_out <= 0 || s_out > sq || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
+  if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (dtype != VSA_BF16 && dtype != VSA_F16) return dtype == VSA_F32 ? VSA_ERR_UNSUPPORTED : VSA_ERR_DTYPE;
   hipStream_t s = (hipStream_t)stream;
 #define VSA_DQ_TILED_CASE(DD, BB)                                                            \
   if (D == DD && be == BB) {                                                                 \
     if (BB == 256 && bh * (sq / 256) >= 256)                                                 \
       return launch_dq_pp<T, DD, true>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, \
-                                       q_vbs, bh, sq, skv, topk, scale, s, slot_rows, s_out); \
+                                       q_vbs, bh, sq, skv, topk, scale, s, slot_rows, s_out, heads); \
     return launch_dq<T, DD, BB, true>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, \
-                                      q_vbs, bh, sq, skv, topk, scale, s, slot_rows, s_out);  \
+                                      q_vbs, bh, sq, skv, topk, scale, s, slot_rows, s_out, heads);  \
   }
   VSA_DISPATCH_MFMA(dtype, T, { VSA_TILED_SHAPES(VSA_DQ_TILED_CASE) });
 #undef VSA_DQ_TILED_CASE
@@ -1334,7 +1335,7 @@ extern "C" int vsa_sparse_bwd_dkdv_tiled(const void* q, const void* k, const voi
                                          const int32_t* counts, const int32_t* offsets,
                                          const int32_t* inverse, const int32_t* kv_vbs, void* dk,
                                          void* dv, const void* d_k_c, const void* d_v_c,
-                                         const int32_t* slot_rows, int64_t s_out, int64_t bh,
+                                         const int32_t* slot_rows, int64_t s_out, int32_t heads, int64_t bh,
                                          int64_t sq, int64_t skv, int32_t D, int32_t be,
                                          int32_t topk, float scale, int32_t* tile_order,
                                          int32_t dtype, void* stream) {
@@ -1345,13 +1346,14 @@ extern "C" int vsa_sparse_bwd_dkdv_tiled(const void* q, const void* k, const voi
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       s_out <= 0 || s_out > skv || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
+  if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (dtype != VSA_BF16 && dtype != VSA_F16) return dtype == VSA_F32 ? VSA_ERR_UNSUPPORTED : VSA_ERR_DTYPE;
   hipStream_t s = (hipStream_t)stream;
 #define VSA_DKDV_TILED_CASE(DD, BB)                                                          \
   if (D == DD && be == BB)                                                                   \
     return launch_dkdv<T, DD, BB, true>(q, k, v, dout, lse, delta, counts, offsets, inverse, \
                                         kv_vbs, dk, dv, d_k_c, d_v_c, bh, sq, skv, topk,     \
-                                        scale, tile_order, s, slot_rows, s_out);
+                                        scale, tile_order, s, slot_rows, s_out, heads);
   VSA_DISPATCH_MFMA(dtype, T, { VSA_TILED_SHAPES(VSA_DKDV_TILED_CASE) });
 #undef VSA_DKDV_TILED_CASE
   return VSA_ERR_UNSUPPORTED;

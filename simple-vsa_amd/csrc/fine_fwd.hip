@@ -57,7 +57,7 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
                                              const T* __restrict__ outc,
                                              const T* __restrict__ gate, int gate_mode,
                                              int gate_heads, const int32_t* __restrict__ orows = nullptr,
-                                             int64_t s_out = 0) {
+                                             int64_t s_out = 0, int heads = 0) {
   using E = Elem<T>;
   const float ltot = pair_sum32(lsum);
   const float inv = 1.0f / ltot;
@@ -65,7 +65,7 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
   int64_t otok = tok;  // row of the combined output and of the gate
   if constexpr (RASTER) {
     const int r = orows[myq];
-    otok = (r >= 0 && r < s_out) ? (int64_t)b * s_out + r : -1;
+    otok = (r >= 0 && r < s_out) ? raster_row(b, r, s_out, heads) : -1;
   }
   const bool ostore = !RASTER || otok >= 0;
   const T* ocrow = outc ? outc + ((int64_t)b * qb + qblk) * D : nullptr;
@@ -141,7 +141,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
     const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles, int tiles_per_head, int sq,
     int skv, int qb, int kb, int topk, float c2, uint32_t qsign, const int32_t* __restrict__ orows,
-    int64_t s_out) {
+    int64_t s_out, int heads) {
   using C = FwdCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   }
 
   fwd_epilogue<T, D, RASTER>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate,
-                             gate_mode, gate_heads, orows, s_out);
+                             gate_mode, gate_heads, orows, s_out, heads);
 }
 
 // ---------------------------------------------------------------------------
@@ -311,7 +311,7 @@ __device__ __forceinline__ void fwd_pp_tile(
     const int32_t* __restrict__ selected, const int32_t* __restrict__ kv_vbs,
     T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
     const T* __restrict__ gate, int gate_mode, int gate_heads, int sq, int skv, int qb, int kb,
-    int topk, float c2, uint32_t qsign, const int32_t* __restrict__ orows, int64_t s_out) {
+    int topk, float c2, uint32_t qsign, const int32_t* __restrict__ orows, int64_t s_out, int heads) {
   constexpr int BE = 256;
   using C = FwdPPCfg<D>;
   using E = Elem<T>;
@@ -351,13 +351,16 @@ __device__ __forceinline__ void fwd_pp_tile(
   bool pvalid = route.next(ps, pc, pkv, pnvb);
   // Copy the cursor's chunk into stage stg; returns its valid keys (0: the
   // route is exhausted and nothing is copied).
+  // the ring's LDS base, converted once (an address-space conversion inside
+  // the loop also costs a null check per copy)
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(smem));
   auto issue = [&](int stg) {
     int nv = 0;
     if (pvalid) {
       const int64_t off = ((int64_t)pkv * BE + pc * C::KC) * D;
-      T* Ks = smem + stg * C::STAGE;
-      tdma.copy(Ks, kbase + off, wave);
-      tdma.copy(Ks + C::TILE, vbase + off, wave);
+      const uint32_t ks = ring_lds + (uint32_t)(stg * C::STAGE * (int)sizeof(T));
+      tdma.copy_lds(ks, kbase + off, wave);
+      tdma.copy_lds(ks + (uint32_t)(C::TILE * (int)sizeof(T)), vbase + off, wave);
       nv = min(pnvb - pc * C::KC, C::KC);
       ++pc;
       pvalid = route.next(ps, pc, pkv, pnvb);
@@ -621,7 +624,7 @@ __device__ __forceinline__ void fwd_pp_tile(
   }
   if (!grp1) phase_barrier();
   fwd_epilogue<T, D, RASTER>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate,
-                             gate_mode, gate_heads, orows, s_out);
+                             gate_mode, gate_heads, orows, s_out, heads);
 }
 
 // Persistent: as many workgroups as the CUs hold (one each), every query block
@@ -635,7 +638,7 @@ sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
                      T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
                      const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles,
                      int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
-                     const int32_t* __restrict__ orows, int64_t s_out) {
+                     const int32_t* __restrict__ orows, int64_t s_out, int heads) {
   using C = FwdPPCfg<D>;
   __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
   const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
@@ -643,7 +646,7 @@ sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
     const int tile = xcd * per + j;
     if (tile >= num_tiles) break;
     fwd_pp_tile<T, D, RASTER>(smem, tile, q, k, v, selected, kv_vbs, out, fine, lse, outc, gate,
-                              gate_mode, gate_heads, sq, skv, qb, kb, topk, c2, qsign, orows, s_out);
+                              gate_mode, gate_heads, sq, skv, qb, kb, topk, c2, qsign, orows, s_out, heads);
     dma_wait();
     __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
   }
@@ -654,7 +657,7 @@ static int launch_fwd_pp(const void* q, const void* k, const void* v, const int3
                          const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* outc,
                          const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq,
                          int64_t skv, int topk, float scale, hipStream_t stream,
-                         const int32_t* orows = nullptr, int64_t s_out = 0) {
+                         const int32_t* orows = nullptr, int64_t s_out = 0, int heads = 0) {
   const int64_t tiles = bh * (sq / 256);
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   const int64_t want = ((tiles + 7) / 8) * 8;
@@ -665,7 +668,7 @@ static int launch_fwd_pp(const void* q, const void* k, const void* v, const int3
   hipLaunchKernelGGL((sparse_fwd_pp_kernel<T, D, RASTER>), dim3(grid), dim3(512), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, (T*)fine, lse,
                      (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, (int)sq,
-                     (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign, orows, s_out);
+                     (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign, orows, s_out, heads);
   return vsa_check_launch();
 }
 
@@ -674,7 +677,7 @@ static int launch_fwd(const void* q, const void* k, const void* v, const int32_t
                       const int32_t* kv_vbs, void* out, void* fine, float* lse, const void* outc,
                       const void* gate, int gate_mode, int gate_heads, int64_t bh, int64_t sq, int64_t skv,
                       int topk, float scale, hipStream_t stream, const int32_t* orows = nullptr,
-                      int64_t s_out = 0) {
+                      int64_t s_out = 0, int heads = 0) {
   using C = FwdCfg<D, BE>;
   const int tph = (int)(sq / C::QT);
   const int64_t tiles = bh * tph;
@@ -685,7 +688,7 @@ static int launch_fwd(const void* q, const void* k, const void* v, const int32_t
   hipLaunchKernelGGL((sparse_fwd_kernel<T, D, BE, RASTER>), dim3(grid), dim3(C::NT), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, (T*)fine, lse,
                      (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, tph, (int)sq,
-                     (int)skv, (int)(sq / BE), (int)(skv / BE), topk, c2, qsign, orows, s_out);
+                     (int)skv, (int)(sq / BE), (int)(skv / BE), topk, c2, qsign, orows, s_out, heads);
   return vsa_check_launch();
 }
 
@@ -764,17 +767,17 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
     if (BB == 256 && bh * (sq / 256) >= 256)                                                   \
       return launch_fwd_pp<T, DD, true>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c,  \
                                         gate, gate_mode, 0, bh, sq, skv, topk, scale, s,       \
-                                        slot_rows, s_out);                                     \
+                                        slot_rows, s_out, heads);                                     \
     return launch_fwd<T, DD, BB, true>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c,   \
                                        gate, gate_mode, 0, bh, sq, skv, topk, scale, s,        \
-                                       slot_rows, s_out);                                      \
+                                       slot_rows, s_out, heads);                                      \
   }
 
 extern "C" int vsa_sparse_fwd_tiled(const void* q, const void* k, const void* v,
                                     const int32_t* selected, const int32_t* kv_vbs, void* out,
                                     void* fine_out, float* lse, const void* out_c,
                                     const void* gate, int32_t gate_mode,
-                                    const int32_t* slot_rows, int64_t s_out, int64_t bh,
+                                    const int32_t* slot_rows, int64_t s_out, int32_t heads, int64_t bh,
                                     int64_t sq, int64_t skv, int32_t D, int32_t be, int32_t topk,
                                     float scale, int32_t dtype, void* stream) {
   if (!q || !k || !v || !selected || !kv_vbs || !out || !slot_rows) return VSA_ERR_NULL;
@@ -787,6 +790,7 @@ extern "C" int vsa_sparse_fwd_tiled(const void* q, const void* k, const void* v,
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       s_out <= 0 || s_out > sq || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
+  if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (dtype == VSA_F32) return VSA_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
   VSA_DISPATCH_MFMA(dtype, T, {

@@ -81,6 +81,15 @@ __device__ __forceinline__ typename Elem<T>::vec8 as_vec8(u32x4 x) {
   return __builtin_bit_cast(typename Elem<T>::vec8, x);
 }
 
+// Token r of head bh in a raster-order sequence of s_out tokens: head-major
+// [B*H, s_out, ...] rows when heads == 0, token-major [B, s_out, H, ...] rows
+// (the layout a projection writes) when heads == H.
+__device__ __forceinline__ int64_t raster_row(int64_t bh, int r, int64_t s_out, int heads) {
+  if (heads == 0) return bh * s_out + r;
+  const int b = (int)bh;  // batch*heads < 2^31 (the entry points check it)
+  return ((int64_t)(b / heads) * s_out + r) * heads + b % heads;
+}
+
 // Streaming global accesses for data a pass touches once: non-temporal loads
 // of the token rows in the block means, the backward preprocessing and the
 // fp32-gate combine, loads and 16-byte stores of the row moves (8-12 % faster
@@ -330,6 +339,13 @@ struct TileDma {
   // temporary of the thread index stays live across the caller's loop)
   __device__ __forceinline__ void copy(T* dst, const T* src, int wave) const {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(dst)) + (uint32_t)wave * 1024u;
+#pragma unroll
+    for (int i = 0; i < N; ++i) dma16_s(voff[i], src, base + (uint32_t)i * (NT / 64) * 1024u);
+  }
+  // copy() to the tile at LDS byte address `dst` (wave-uniform), for callers
+  // that convert their LDS base once outside the loop
+  __device__ __forceinline__ void copy_lds(uint32_t dst, const T* src, int wave) const {
+    const uint32_t base = dst + (uint32_t)wave * 1024u;
 #pragma unroll
     for (int i = 0; i < N; ++i) dma16_s(voff[i], src, base + (uint32_t)i * (NT / 64) * 1024u);
   }

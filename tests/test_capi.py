@@ -95,31 +95,34 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     # tiled-sequence entry points validate before launching
     assert lib.vsa_tile_slot_rows(0, 4, 4, 2, 2, 2, p, None) == -2
     assert lib.vsa_tile_slot_rows(4, 4, 4, 2, 2, 2, None, None) == -1
-    assert lib.vsa_tile_pool_qkv(*([p] * 10 + [None]), 1, 64, 1, 128, 64, 0, None) == -1
-    assert lib.vsa_tile_pool_qkv(*([p] * 11), 1, 65, 1, 128, 64, 0, None) == -2  # s_out > nb*be
+    assert lib.vsa_tile_pool_qkv(*([p] * 10 + [None]), 1, 64, 0, 1, 128, 64, 0, None) == -1
+    assert lib.vsa_tile_pool_qkv(*([p] * 11), 1, 65, 0, 1, 128, 64, 0, None) == -2  # s_out > nb*be
+    assert lib.vsa_tile_pool_qkv(*([p] * 11), 3, 64, 2, 1, 128, 64, 0, None) == -2  # 3 % 2 heads
     fwd = [p] * 10
-    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, None, 64, 1, 64, 64, 128, 64, 1, 0.1, 0,
+    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, None, 64, 0, 1, 64, 64, 128, 64, 1, 0.1, 0,
                                     None) == -1                   # no slot_rows
-    assert lib.vsa_sparse_fwd_tiled(*fwd, 3, p, 64, 1, 64, 64, 128, 64, 1, 0.1, 0,
-                                    None) == -2                   # token-major gate
-    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, p, 65, 1, 64, 64, 128, 64, 1, 0.1, 0,
+    assert lib.vsa_sparse_fwd_tiled(*fwd, 3, p, 64, 0, 1, 64, 64, 128, 64, 1, 0.1, 0,
+                                    None) == -2                   # gate mode 3
+    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, p, 65, 0, 1, 64, 64, 128, 64, 1, 0.1, 0,
                                     None) == -2                   # s_out > tiled length
-    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, p, 64, 1, 64, 64, 256, 64, 1, 0.1, 0,
+    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, p, 64, 2, 3, 64, 64, 128, 64, 1, 0.1, 0,
+                                    None) == -2                   # heads must divide bh
+    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, p, 64, 0, 1, 64, 64, 256, 64, 1, 0.1, 0,
                                     None) == -4                   # head_dim 256: composition
-    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, p, 64, 1, 64, 64, 128, 64, 1, 0.1, 2,
+    assert lib.vsa_sparse_fwd_tiled(*fwd, 1, p, 64, 0, 1, 64, 64, 128, 64, 1, 0.1, 2,
                                     None) == -4                   # fp32: composition
-    assert lib.vsa_bwd_prep_tiled(p, p, p, p, 1, p, 64, p, p, p, None, 1, 64, 128, 64, 0,
+    assert lib.vsa_bwd_prep_tiled(p, p, p, p, 1, p, 64, 0, p, p, p, None, 1, 64, 128, 64, 0,
                                   None) == -1                     # no dout_t
-    assert lib.vsa_bwd_prep_tiled(p, p, p, p, 3, p, 64, p, p, p, p, 1, 64, 128, 64, 0,
+    assert lib.vsa_bwd_prep_tiled(p, p, p, p, 3, p, 64, 0, p, p, p, p, 1, 64, 128, 64, 0,
                                   None) == -2
-    assert lib.vsa_sparse_bwd_dq_tiled(*([p] * 11), None, 64, 1, 64, 64, 128, 64, 1, 0.1, 0,
+    assert lib.vsa_sparse_bwd_dq_tiled(*([p] * 11), None, 64, 0, 1, 64, 64, 128, 64, 1, 0.1, 0,
                                        None) == -1
-    assert lib.vsa_sparse_bwd_dq_tiled(*([p] * 12), 64, 1, 64, 64, 128, 96, 1, 0.1, 0,
+    assert lib.vsa_sparse_bwd_dq_tiled(*([p] * 12), 64, 0, 1, 64, 64, 128, 96, 1, 0.1, 0,
                                        None) == -2               # 64 % 96
-    assert lib.vsa_sparse_bwd_dkdv_tiled(*([p] * 14), None, 64, 1, 64, 64, 128, 64, 1, 0.1,
+    assert lib.vsa_sparse_bwd_dkdv_tiled(*([p] * 14), None, 64, 0, 1, 64, 64, 128, 64, 1, 0.1,
                                          None, 0, None) == -1
-    assert lib.vsa_sparse_bwd_dkdv_tiled(*([p] * 15), 64, 1, 64, 64, 128, 64, 1, 0.1, None, 7,
-                                         None) == -3             # no dtype 7
+    assert lib.vsa_sparse_bwd_dkdv_tiled(*([p] * 15), 64, 0, 1, 64, 64, 128, 64, 1, 0.1, None,
+                                         7, None) == -3          # no dtype 7
 
 
 def _full(nb, be):

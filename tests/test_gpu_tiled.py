@@ -138,3 +138,27 @@ def test_fused_tiled_op_at_c3_size_equals_the_composition():
         del out, grads, leaves
     for name, a, b in zip(["out", "dq", "dk", "dv", "dgate"], *outs):
         assert torch.equal(a, b), (name, (a.float() - b.float()).abs().max().item())
+
+
+@pytest.mark.parametrize("case", [0, 1])
+def test_token_major_tiled_op_equals_head_major_and_composition(case):
+    """q, k, v, gate, dout as [B, S, H, D] (the projection's layout, tile()'s
+    [batch, seq, ...]): the same values as the head-major op, transposed, and
+    as tile -> op -> untile along dim 1."""
+    from vsa_mi355x import tiled, tiling
+    shape, ts, heads, d, dtype, gate, topk = CASES[case]
+    q, k, v, do, gt = _inputs(shape, heads, d, dtype, gate, seed=77 + case)
+    tm = (lambda x: None if x is None else x.transpose(1, 2).contiguous())
+    head_major = _run(lambda q_, k_, v_, g_: tiled.mi355x_vsa_tiled(q_, k_, v_, shape, topk, ts, g_),
+                      q, k, v, do, gt)
+    token_major = _run(lambda q_, k_, v_, g_: tiled.mi355x_vsa_tiled(
+        q_, k_, v_, shape, topk, ts, g_, token_major=True), tm(q), tm(k), tm(v), tm(do), tm(gt))
+    meta = tiling.build_vsa_metadata(shape, ts, device=DEV)
+    nb = math.prod([math.ceil(a / b) for a, b in zip(shape, ts)])
+    ref = _run(lambda q_, k_, v_, g_: tiled._composition(q_, k_, v_, meta, nb, math.prod(ts), ts,
+                                                         topk, g_, token_major=True),
+               tm(q), tm(k), tm(v), tm(do), tm(gt))
+    for name, a, b, c in zip(["out", "dq", "dk", "dv", "dgate"], head_major, token_major, ref):
+        assert b.shape == c.shape, name
+        assert torch.equal(b, c), (name, "token-major vs composition")
+        assert torch.equal(a.transpose(1, 2), b), (name, "token-major vs head-major")

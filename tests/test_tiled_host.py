@@ -38,3 +38,12 @@ def test_gate_must_broadcast_to_q():
 def test_cpu_tensors_are_rejected():
     with pytest.raises(ValueError, match="requires GPU tensors"):
         tiled.mi355x_vsa_tiled(*_qkv(120), (4, 5, 6), 2, (4, 4, 4))
+
+
+def test_token_major_sequence_length_is_dim_one():
+    q, k, v = _qkv(120)
+    with pytest.raises(ValueError, match=r"seq_len 2 is not T\*H\*W"):
+        tiled.mi355x_vsa_tiled(q, k, v, (4, 5, 6), 2, token_major=True)
+    tm = [x.transpose(1, 2).contiguous() for x in (q, k, v)]
+    with pytest.raises(ValueError, match="requires GPU tensors"):
+        tiled.mi355x_vsa_tiled(*tm, (4, 5, 6), 2, token_major=True)
