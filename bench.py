@@ -336,6 +336,54 @@ def run_tiled(steps, warmup):
     return res
 
 
+def run_views(steps, warmup):
+    """c3 as a DiT's projections hand it over: q, k, v and the gate are
+    [B, H, S, D] views of token-major [B, S, H, D] tensors (the gate producer's
+    view, common.py:326-328) and the output is consumed as [B, S, H*D].
+    fwd+bwd of mi355x_vsa reading the views in place against the same op on
+    contiguous copies (what a contiguous-only kernel needs: three copies in,
+    one out, and the same again for the gradients)."""
+    import torch
+    from vsa_mi355x import mi355x as M
+    B, H, S, D, topk = CFG["B"], CFG["H"], CFG["S"], CFG["D"], CFG["topk"]
+    be = math.prod(CFG["block"])
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    base = [torch.randn(B, S, H, D, generator=g, device=dev, dtype=torch.bfloat16)
+            for _ in range(3)]
+    gbase = torch.rand(B, S, H, D, generator=g, device=dev, dtype=torch.bfloat16)
+    do = torch.randn(B, S, H * D, generator=g, device=dev, dtype=torch.bfloat16)
+    leaves = [t.requires_grad_() for t in (*base, gbase)]
+    vbs = torch.full((S // be,), be, dtype=torch.int32, device=dev)
+    res = {"workload": "views", "B": B, "H": H, "S": S, "D": D, "block": list(CFG["block"]),
+           "topk": topk}
+
+    def views():
+        q, k, v, gate = (x.transpose(1, 2) for x in leaves)
+        return M.mi355x_vsa(q, k, v, vbs, vbs, topk, CFG["block"], gate)
+
+    def copies():
+        q, k, v, gate = (x.transpose(1, 2) for x in leaves)
+        return M.mi355x_vsa(q.contiguous(), k.contiguous(), v.contiguous(), vbs, vbs, topk,
+                            CFG["block"], gate)
+
+    for name, fwd in (("views", views), ("copies", copies)):
+        def step(fwd=fwd):
+            out = fwd().transpose(1, 2).reshape(B, S, H * D)
+            torch.autograd.grad(out, leaves, do)
+
+        def fwd_only(fwd=fwd):
+            with torch.no_grad():
+                fwd().transpose(1, 2).reshape(B, S, H * D)
+        for _ in range(warmup):
+            step()
+        res[name + "_fwd_bwd_ms"] = round(_events_time(step, steps), 3)
+        res[name + "_fwd_ms"] = round(_events_time(fwd_only, steps), 3)
+    res["saved_fwd_bwd_ms"] = round(res["copies_fwd_bwd_ms"] - res["views_fwd_bwd_ms"], 3)
+    res["saved_fwd_ms"] = round(res["copies_fwd_ms"] - res["views_fwd_ms"], 3)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -350,7 +398,8 @@ def main():
                          "reported under 'workloads' of the c3 line; 0 skips them")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads of the workload timed on the CPU oracle (one at a time)")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["tiling", "gate", "tiled"],
+    ap.add_argument("--workload",
+                    choices=sorted(WORKLOADS) + ["tiling", "gate", "tiled", "views"],
                     default="c3",
                     help="BASELINE configuration to run (c3 is the metric's workload)")
     args = ap.parse_args()
@@ -381,6 +430,9 @@ def main():
         return
     if args.workload == "tiled":
         print(json.dumps(run_tiled(args.steps, args.warmup)), flush=True)
+        return
+    if args.workload == "views":
+        print(json.dumps(run_views(args.steps, args.warmup)), flush=True)
         return
     if args.workload != "c3":
         print(json.dumps(run_workload(args.workload, args.steps, args.warmup)), flush=True)

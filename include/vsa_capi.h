@@ -322,10 +322,14 @@ int vsa_tile_slot_rows(int32_t T, int32_t H, int32_t W, int32_t ts, int32_t hs, 
  * tile() of q, k, v [bh, s_out, D] into q_t, k_t, v_t [bh, nb*be, D] (zero rows
  * at padding slots) and the padded block mean of the tiled copies into
  * q_c, k_c, v_c [bh, nb, D], in one pass: vsa_pool_qkv after tile()
- * (fused_block_mean, fused_common.py:20-59, on tile's output).
+ * (fused_block_mean, fused_common.py:20-59, on tile's output), q's means
+ * over q_variable_block_sizes, k's and v's over kv_variable_block_sizes.
+ * With slot_rows[s] = s (tokens already in block order, s_out = nb*be) this
+ * is vsa_pool_qkv reading token-major q, k, v in place.
  */
 int vsa_tile_pool_qkv(const void* q, const void* k, const void* v, const int32_t* slot_rows,
-                      const int32_t* variable_block_sizes, void* q_t, void* k_t, void* v_t,
+                      const int32_t* q_variable_block_sizes,
+                      const int32_t* kv_variable_block_sizes, void* q_t, void* k_t, void* v_t,
                       void* q_c, void* k_c, void* v_c, int64_t bh, int64_t s_out, int32_t heads,
                       int32_t nb, int32_t head_dim, int32_t block_elements, int32_t dtype,
                       void* stream);

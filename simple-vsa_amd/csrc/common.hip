@@ -88,7 +88,8 @@ __global__ __launch_bounds__(256) void pool_qkv_kernel(
 template <typename T>
 __global__ __launch_bounds__(256) void tile_pool_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int32_t* __restrict__ rows, const int32_t* __restrict__ vbs, T* __restrict__ qt,
+    const int32_t* __restrict__ rows, const int32_t* __restrict__ q_vbs,
+    const int32_t* __restrict__ kv_vbs, T* __restrict__ qt,
     T* __restrict__ kt, T* __restrict__ vt, T* __restrict__ qc, T* __restrict__ kc,
     T* __restrict__ vc, int64_t bh, int nb, int D, int be, int64_t s_out, int heads) {
   constexpr int VEC = 16 / sizeof(T);
@@ -98,10 +99,11 @@ __global__ __launch_bounds__(256) void tile_pool_kernel(
   const T* x = q;
   T* xt = qt;
   T* out = qc;
+  const int32_t* vbs = q_vbs;
   if (id >= 2 * per) {
-    id -= 2 * per; x = v; xt = vt; out = vc;
+    id -= 2 * per; x = v; xt = vt; out = vc; vbs = kv_vbs;
   } else if (id >= per) {
-    id -= per; x = k; xt = kt; out = kc;
+    id -= per; x = k; xt = kt; out = kc; vbs = kv_vbs;
   }
   const int n = (int)(id % nb);
   const int64_t head = id / nb;
@@ -637,11 +639,13 @@ extern "C" int vsa_pool_qkv(const void* q, const void* k, const void* v, const i
 }
 
 extern "C" int vsa_tile_pool_qkv(const void* q, const void* k, const void* v,
-                                 const int32_t* slot_rows, const int32_t* vbs, void* q_t,
+                                 const int32_t* slot_rows, const int32_t* q_vbs,
+                                 const int32_t* kv_vbs, void* q_t,
                                  void* k_t, void* v_t, void* q_c, void* k_c, void* v_c,
                                  int64_t bh, int64_t s_out, int32_t heads, int32_t nb, int32_t D,
                                  int32_t be, int32_t dtype, void* stream) {
-  if (!q || !k || !v || !slot_rows || !vbs || !q_t || !k_t || !v_t || !q_c || !k_c || !v_c)
+  if (!q || !k || !v || !slot_rows || !q_vbs || !kv_vbs || !q_t || !k_t || !v_t || !q_c ||
+      !k_c || !v_c)
     return VSA_ERR_NULL;
   if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (bh <= 0 || nb <= 0 || be <= 0 || be > 256 || s_out <= 0 || s_out > (int64_t)nb * be ||
@@ -652,7 +656,8 @@ extern "C" int vsa_tile_pool_qkv(const void* q, const void* k, const void* v,
   hipStream_t s = (hipStream_t)stream;
   VSA_DISPATCH_ALL(dtype, T, {
     hipLaunchKernelGGL(tile_pool_kernel<T>, dim3((unsigned)grid), dim3(256), 0, s, (const T*)q,
-                       (const T*)k, (const T*)v, slot_rows, vbs, (T*)q_t, (T*)k_t, (T*)v_t,
+                       (const T*)k, (const T*)v, slot_rows, q_vbs, kv_vbs, (T*)q_t, (T*)k_t,
+                       (T*)v_t,
                        (T*)q_c, (T*)k_c, (T*)v_c, bh, nb, D, be, s_out, heads);
   });
   return vsa_check_launch();

@@ -51,8 +51,8 @@ SIGNATURES = {
     "vsa_rows_zero_unmarked": [_P, _I64, _I64, _I64, _P, _I64, _P, _P],
     # tiled sequences (tile / untile fused into the op)
     "vsa_tile_slot_rows": [_I32, _I32, _I32, _I32, _I32, _I32, _P, _P],
-    "vsa_tile_pool_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32,
-                          _I32, _I32, _I32, _P],
+    "vsa_tile_pool_qkv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32,
+                          _I32, _I32, _I32, _I32, _P],
     "vsa_sparse_fwd_tiled": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _I64, _I32, _I64,
                              _I64, _I64, _I32, _I32, _I32, _F, _I32, _P],
     "vsa_bwd_prep_tiled": [_P, _P, _P, _P, _I32, _P, _I64, _I32, _P, _P, _P, _P, _I64, _I64, _I32,

@@ -285,6 +285,19 @@ def _token_major(gate: Tensor) -> bool:
     return gate.stride() == (s * h * d, d, h * d, 1) and not gate.is_contiguous()
 
 
+def _raster_views(q, k, v, gate, be) -> bool:
+    """True when q, k and v are [B, H, S, D] views of token-major [B, S, H, D]
+    memory (a DiT's per-head view of its projection output, as the gate
+    producer returns one, common.py:326-328) that the raster kernels read and
+    write in place: one sequence length for q and kv, bf16 / fp16, head dim 64
+    or 128, a block volume with its own kernel and a gate (if any) in q's dtype."""
+    if q.shape != k.shape or not all(_token_major(x) for x in (q, k, v)):
+        return False
+    if q.dtype not in MFMA_DTYPES or q.shape[-1] not in (64, 128) or be not in SUPPORTED_BLOCKS:
+        return False
+    return gate is None or gate.dtype == q.dtype
+
+
 def _gate_mode(gate: Optional[Tensor], d: int, dtype: torch.dtype) -> int:
     """C-ABI gate mode: layout, plus the fp32 flag for an fp32 gate beside
     bf16 / fp16 inputs."""
@@ -513,7 +526,10 @@ def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
     """Video Sparse Attention on MI355X: ``out = out_c * gate + out_s``
     (torch_impl.py:49-113), coarse routing by Top-K of the pooled scores.
 
-    Top-K ties are resolved towards the smaller key-block id."""
+    Top-K ties are resolved towards the smaller key-block id.  When q, k and v
+    are per-head views of token-major [B, S, H, D] tensors the kernels read
+    them in place and the result is the same kind of view (no copies either
+    side); values are the same bit for bit."""
     be = as_block_elements(block_size)
     validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
     _check_device_path(q, k, v, be)
@@ -522,6 +538,9 @@ def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
     vbs = _i32(variable_block_sizes, q.device)
     qvbs = _i32(q_variable_block_sizes, q.device)
     with torch.cuda.device(q.device):
+        if _raster_views(q, k, v, gate, be):
+            from . import tiled
+            return tiled.vsa_token_major_views(q, k, v, gate, vbs, qvbs, topk, be, scale)
         pads = _padded(q, k, be)
         if pads is not None:
             kbe, kd, pad_q, pad_k, unpad_out = pads

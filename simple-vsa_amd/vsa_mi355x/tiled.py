@@ -72,21 +72,21 @@ def _dims(x, token_major):
     return tuple(x.shape)
 
 
-def _tile_pool(q, k, v, rows, vbs, nb, be, token_major):
+def _tile_pool(q, k, v, rows, qvbs, vbs, nb, be, token_major):
     b, h, s_out, d = _dims(q, token_major)
     tiled = (b, h, nb * be, d)
     qt, kt, vt = (torch.empty(tiled, device=q.device, dtype=q.dtype) for _ in range(3))
     qc, kc, vc = (torch.empty((b, h, nb, d), device=q.device, dtype=q.dtype) for _ in range(3))
     _lib.call("vsa_tile_pool_qkv", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(rows),
-              _lib.ptr(vbs), _lib.ptr(qt), _lib.ptr(kt), _lib.ptr(vt), _lib.ptr(qc),
+              _lib.ptr(qvbs), _lib.ptr(vbs), _lib.ptr(qt), _lib.ptr(kt), _lib.ptr(vt), _lib.ptr(qc),
               _lib.ptr(kc), _lib.ptr(vc), b * h, s_out, h if token_major else 0, nb, d, be,
               _lib.dtype_code(q.dtype), _lib.stream_of(q))
     return qt, kt, vt, qc, kc, vc
 
 
-def _forward(q, k, v, gate, rows, vbs, topk, nb, be, scale, want_lse, token_major):
+def _forward(q, k, v, gate, rows, vbs, qvbs, topk, nb, be, scale, want_lse, token_major):
     b, h, s_out, d = _dims(q, token_major)
-    qt, kt, vt, qc, kc, vc = _tile_pool(q, k, v, rows, vbs, nb, be, token_major)
+    qt, kt, vt, qc, kc, vc = _tile_pool(q, k, v, rows, qvbs, vbs, nb, be, token_major)
     _, probs, outc, sel = M.coarse_forward(qc, kc, vc, topk, scale)
     L = nb * be
     out = torch.empty_like(q)
@@ -102,15 +102,17 @@ def _forward(q, k, v, gate, rows, vbs, topk, nb, be, scale, want_lse, token_majo
 
 class _VSATiled(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, gate, rows, vbs, topk_, nb, be, scale, token_major):
-        out, saved = _forward(q, k, v, gate, rows, vbs, topk_, nb, be, scale, True, token_major)
-        ctx.save_for_backward(gate, rows, vbs, *saved)
+    def forward(ctx, q, k, v, gate, rows, vbs, qvbs, topk_, nb, be, scale, token_major):
+        out, saved = _forward(q, k, v, gate, rows, vbs, qvbs, topk_, nb, be, scale, True,
+                              token_major)
+        ctx.save_for_backward(gate, rows, vbs, qvbs, *saved)
         ctx.dims = (q.shape, _dims(q, token_major), nb, be, scale, token_major)
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        gate, rows, vbs, qt, kt, vt, qc, kc, vc, probs, outc, sel, fine, lse = ctx.saved_tensors
+        gate, rows, vbs, qvbs, qt, kt, vt, qc, kc, vc, probs, outc, sel, fine, lse = \
+            ctx.saved_tensors
         shape, (b, h, s_out, d), nb, be, scale, token_major = ctx.dims
         heads = h if token_major else 0
         L = nb * be
@@ -131,7 +133,7 @@ class _VSATiled(torch.autograd.Function):
         dk, dv = torch.empty_like(dq), torch.empty_like(dq)
         _lib.call("vsa_sparse_bwd_dq_tiled", _lib.ptr(qt), _lib.ptr(kt), _lib.ptr(vt),
                   _lib.ptr(dout_t), _lib.ptr(lse), _lib.ptr(delta), _lib.ptr(sel), _lib.ptr(vbs),
-                  _lib.ptr(dq), _lib.ptr(dqc), _lib.ptr(vbs), _lib.ptr(rows), s_out, heads, b * h,
+                  _lib.ptr(dq), _lib.ptr(dqc), _lib.ptr(qvbs), _lib.ptr(rows), s_out, heads, b * h,
                   L, L, d, be, tk, float(scale), code, stream)
         inverse, offsets, counts = M.invert_routes(sel, nb)
         order = M.dkdv_tile_order(counts, b * h, L, d, be)
@@ -140,7 +142,36 @@ class _VSATiled(torch.autograd.Function):
                   _lib.ptr(offsets), _lib.ptr(inverse), _lib.ptr(vbs), _lib.ptr(dk), _lib.ptr(dv),
                   _lib.ptr(dkc), _lib.ptr(dvc), _lib.ptr(rows), s_out, heads, b * h, L, L, d, be,
                   tk, float(scale), _lib.ptr(order), code, stream)
-        return dq, dk, dv, d_gate, None, None, None, None, None, None, None
+        return dq, dk, dv, d_gate, None, None, None, None, None, None, None, None
+
+
+@functools.lru_cache(maxsize=16)
+def _identity_rows(n: int, device: torch.device) -> Tensor:
+    """int32 [n]: slot s at raster row s (tokens already in block order)."""
+    return torch.arange(n, dtype=torch.int32, device=device)
+
+
+def vsa_token_major_views(q, k, v, gate, vbs, qvbs, topk, be, scale):
+    """``mi355x_vsa`` on [B, H, S, D] views of token-major [B, S, H, D] q, k, v:
+    the raster kernels with the identity slot table read the token-major
+    memory in place and write the output (and dq, dk, dv, d_gate) token-major,
+    returned as the same kind of view.  A gate is taken token-major too (free
+    for the gate producer's view, one copy for a head-major gate).  The values
+    are those of the op on contiguous copies bit for bit: the pool, prep and
+    epilogue passes sum in the same order whatever the row addressing."""
+    qr, kr, vr = (x.transpose(1, 2) for x in (q, k, v))
+    g = None if gate is None else gate.transpose(1, 2).contiguous()
+    s = qr.shape[1]
+    rows = _identity_rows(s, q.device)
+    needs_grad = torch.is_grad_enabled() and (
+        q.requires_grad or k.requires_grad or v.requires_grad
+        or (g is not None and g.requires_grad))
+    if needs_grad:
+        out = _VSATiled.apply(qr, kr, vr, g, rows, vbs, qvbs, topk, s // be, be, scale, True)
+    else:
+        out = _forward(qr, kr, vr, g, rows, vbs, qvbs, topk, s // be, be, scale, False,
+                       True)[0]
+    return out.transpose(1, 2)
 
 
 def _composition(q, k, v, meta, nb, be, tile_size, topk, gate, token_major=False):
@@ -226,5 +257,7 @@ def mi355x_vsa_tiled(q: Tensor, k: Tensor, v: Tensor, dit_seq_shape: Tuple[int, 
             q.requires_grad or k.requires_grad or v.requires_grad
             or (gate is not None and gate.requires_grad))
         if needs_grad:
-            return _VSATiled.apply(q, k, v, gate, rows, vbs, topk, nb, be, scale, token_major)
-        return _forward(q, k, v, gate, rows, vbs, topk, nb, be, scale, False, token_major)[0]
+            return _VSATiled.apply(q, k, v, gate, rows, vbs, vbs, topk, nb, be, scale,
+                                   token_major)
+        return _forward(q, k, v, gate, rows, vbs, vbs, topk, nb, be, scale, False,
+                        token_major)[0]

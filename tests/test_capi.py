@@ -95,9 +95,9 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     # tiled-sequence entry points validate before launching
     assert lib.vsa_tile_slot_rows(0, 4, 4, 2, 2, 2, p, None) == -2
     assert lib.vsa_tile_slot_rows(4, 4, 4, 2, 2, 2, None, None) == -1
-    assert lib.vsa_tile_pool_qkv(*([p] * 10 + [None]), 1, 64, 0, 1, 128, 64, 0, None) == -1
-    assert lib.vsa_tile_pool_qkv(*([p] * 11), 1, 65, 0, 1, 128, 64, 0, None) == -2  # s_out > nb*be
-    assert lib.vsa_tile_pool_qkv(*([p] * 11), 3, 64, 2, 1, 128, 64, 0, None) == -2  # 3 % 2 heads
+    assert lib.vsa_tile_pool_qkv(*([p] * 11 + [None]), 1, 64, 0, 1, 128, 64, 0, None) == -1
+    assert lib.vsa_tile_pool_qkv(*([p] * 12), 1, 65, 0, 1, 128, 64, 0, None) == -2  # s_out > nb*be
+    assert lib.vsa_tile_pool_qkv(*([p] * 12), 3, 64, 2, 1, 128, 64, 0, None) == -2  # 3 % 2 heads
     fwd = [p] * 10
     assert lib.vsa_sparse_fwd_tiled(*fwd, 1, None, 64, 0, 1, 64, 64, 128, 64, 1, 0.1, 0,
                                     None) == -1                   # no slot_rows

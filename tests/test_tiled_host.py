@@ -47,3 +47,24 @@ def test_token_major_sequence_length_is_dim_one():
     tm = [x.transpose(1, 2).contiguous() for x in (q, k, v)]
     with pytest.raises(ValueError, match="requires GPU tensors"):
         tiled.mi355x_vsa_tiled(*tm, (4, 5, 6), 2, token_major=True)
+
+
+def test_raster_views_rule():
+    """Which [B, H, S, D] inputs mi355x_vsa reads in place as token-major views."""
+    from vsa_mi355x import mi355x as M
+
+    def tm(s=256, h=4, d=128, dtype=torch.bfloat16):
+        return torch.zeros(1, s, h, d, dtype=dtype).transpose(1, 2)
+
+    q, k, v = tm(), tm(), tm()
+    assert M._raster_views(q, k, v, None, 64)
+    assert M._raster_views(q, k, v, tm(), 256)
+    assert M._raster_views(q, k, v, tm(d=1), 128)                      # per-token gate
+    assert M._raster_views(q, k, v, q.contiguous(), 64)                # head-major gate
+    assert not M._raster_views(q.contiguous(), k, v, None, 64)         # head-major q
+    assert not M._raster_views(q, k, v, tm(dtype=torch.float32), 64)   # fp32 gate
+    assert not M._raster_views(q, tm(s=512), tm(s=512), None, 64)      # q / kv lengths differ
+    assert not M._raster_views(tm(d=256), tm(d=256), tm(d=256), None, 64)
+    assert not M._raster_views(*(tm(dtype=torch.float32) for _ in range(3)), None, 64)
+    assert not M._raster_views(q, k, v, None, 32)                      # padded block volume
+    assert not M._raster_views(tm(h=1), tm(h=1), tm(h=1), None, 64)    # one head: contiguous
