@@ -215,9 +215,10 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
 }
 
 // ===========================================================================
-// dK / dV: one workgroup per KV tile of KT keys (wave w owns keys 32w..32w+31,
-// K^T/V^T fragments in VGPRs), looping over the 32-query sub-tiles ("items")
-// of the tile's CSR in-edges.  Per item i the wave computes
+// dK / dV: one workgroup per KV tile of KT keys (wave w owns keys KW w ..
+// KW w + KW - 1 as KTL 32-key MFMA tiles, K^T/V^T fragments in VGPRs),
+// looping over the 32-query sub-tiles ("items") of the tile's CSR in-edges.
+// Per item i the wave computes
 //   A(i): S = Q_i K^T, dP = dO_i V^T             (MFMA, rows of the LDS tiles)
 //   B(i): P = exp2(S c2 - lse), dS = P (dP - delta)          (VALU)
 //   C(i): dV^T += dO_i^T P, dK^T += Q_i^T dS      (MFMA, transposed LDS reads)
@@ -225,12 +226,18 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
 // (an MFMA only overlaps VALU work of its own wave on CDNA4).  One wave per
 // SIMD: the accumulators live in AGPRs, and latency is covered inside the
 // wave by an LDS read stream L operands deep and an NS-stage LDS ring of
-// items filled by direct global->LDS loads spread over each step.
+// items filled by direct global->LDS loads spread over each step.  Every LDS
+// operand read feeds KTL MFMAs (one per key tile of the wave).
 // ===========================================================================
 template <int D, int BE>
 struct DkvCfg {
-  static constexpr int KT = BE >= 128 ? 128 : BE;  // keys per workgroup
-  static constexpr int NW = KT / 32;
+  // keys per wave: 64 at head_dim 64, where the fragments and accumulators of
+  // two key tiles fit one wave's 512 registers and each Q / dO operand read
+  // from LDS then feeds two MFMAs; 32 above
+  static constexpr int KW = D == 64 ? 64 : 32;
+  static constexpr int KTL = KW / 32;              // 32-key MFMA tiles per wave
+  static constexpr int KT = BE < 4 * KW ? BE : 4 * KW;  // keys per workgroup
+  static constexpr int NW = KT / KW;
   static constexpr int NT = NW * 64;
   static constexpr int QS = 32;                    // queries per LDS stage
   static constexpr int TILE = QS * D;              // one Q (or dO) sub-tile, swizzled
@@ -238,16 +245,19 @@ struct DkvCfg {
   static constexpr int NS = 4;                     // LDS ring depth (loop unrolled by NS)
   static constexpr int TP = TILE / 8 / NT;         // direct loads per thread per tile
   static constexpr int PER = 2 * TP + 1;           // direct loads per thread per item
-  static constexpr int SEGMAX = 2048;              // CSR entries staged in LDS
+  // CSR entries staged in LDS (1024 for one-wave workgroups, so that four of
+  // them fit a CU's LDS)
+  static constexpr int SEGMAX = NW == 1 ? 1024 : 2048;
   // dK/dV dims accumulated per workgroup: all of them up to 128; for head_dim
   // 256 two workgroups share a key tile, each computing S and dP over all 256
   // dims and accumulating one 128-dim half of dK and dV (the full accumulators
   // would not fit next to the K and V fragments)
   static constexpr int DH = D > 128 ? 128 : D;
   static constexpr int NSPLIT = D / DH;
-  static constexpr int NA = 2 * (D / 16);          // MFMAs of A (S and dP interleaved)
-  static constexpr int NC = 4 * (DH / 32);         // MFMAs of C (dV and dK interleaved)
-  static constexpr int L = D > 128 ? 6 : 12;       // LDS operand lookahead
+  static constexpr int NA = 2 * (D / 16);          // LDS reads of A (Q and dO rows interleaved)
+  static constexpr int NC = 4 * (DH / 32);         // LDS reads of C (dO^T and Q^T tiles)
+  static constexpr int NV = 16 * KTL;              // P (and dS) values per lane and item
+  static constexpr int L = D > 128 ? 6 : KTL > 1 ? 6 : 12;  // LDS operand lookahead (reads)
 };
 
 template <typename T, int D, int BE>
@@ -275,7 +285,8 @@ __device__ __forceinline__ void dkdv_tile(
   using C = DkvCfg<D, BE>;
   using E = Elem<T>;
   typedef typename E::vec8 V8;
-  constexpr int NS = C::NS, NA = C::NA, NC = C::NC, L = C::L, TP = C::TP;
+  constexpr int NS = C::NS, NA = C::NA, NC = C::NC, L = C::L, TP = C::TP, KTL = C::KTL;
+  constexpr int NV = C::NV;
   auto& smem = sh.smem;
   auto& sstat = sh.sstat;
   auto& sseg = sh.sseg;
@@ -289,23 +300,25 @@ __device__ __forceinline__ void dkdv_tile(
   // on the scalar unit (no per-copy read-back of a vector register)
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int r = lane & 31, h = lane >> 5;
-  const int mykey = k0 + wave * 32 + r;
-  const int64_t ktok = (int64_t)b * skv + mykey;
+  // this lane's key in key tile t: mykey0 + 32 t
+  const int mykey0 = k0 + wave * C::KW + r;
   const int32_t cnt = kv_vbs[kvblk];  // read once: the epilogue's pooled division needs it too
   const int nvb = clamp_valid(cnt, BE);
-  const bool key_valid = (mykey - kvblk * BE) < nvb;
 
-  // K^T, V^T fragments (B operands): lane (r, h) holds key r, dims 16ks + 8h ..
-  V8 kf[D / 16], vf[D / 16];
-  {
+  // K^T, V^T fragments (B operands): lane (r, h) of key tile t holds key
+  // mykey0 + 32 t, dims 16ks + 8h ..
+  V8 kf[KTL][D / 16], vf[KTL][D / 16];
+#pragma unroll
+  for (int t = 0; t < KTL; ++t) {
+    const int64_t ktok = (int64_t)b * skv + mykey0 + 32 * t;
     const T* krow = k + ktok * D + 8 * h;
     const T* vrow = v + ktok * D + 8 * h;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
       u32x4 raw = *reinterpret_cast<const u32x4*>(krow + 16 * ks);
       raw ^= ksign;
-      kf[ks] = as_vec8<T>(raw);
-      vf[ks] = as_vec8<T>(*reinterpret_cast<const u32x4*>(vrow + 16 * ks));
+      kf[t][ks] = as_vec8<T>(raw);
+      vf[t][ks] = as_vec8<T>(*reinterpret_cast<const u32x4*>(vrow + 16 * ks));
     }
   }
 
@@ -397,13 +410,15 @@ __device__ __forceinline__ void dkdv_tile(
   // compiler shares one zero register between them and the S / dP tiles and
   // then moves two dK/dV accumulators aside every step to make room for S/dP
   // (about 16 extra accumulator moves per step, and a spill at head_dim 256).
-  f32x16 dkacc[C::DH / 32], dvacc[C::DH / 32];
+  f32x16 dkacc[C::DH / 32][KTL], dvacc[C::DH / 32][KTL];
 #pragma unroll
-  for (int mt = 0; mt < C::DH / 32; ++mt) {
-    dkacc[mt] = f32x16{};
-    dvacc[mt] = f32x16{};
-    asm volatile("" : "+a"(dkacc[mt]), "+a"(dvacc[mt]));
-  }
+  for (int mt = 0; mt < C::DH / 32; ++mt)
+#pragma unroll
+    for (int t = 0; t < KTL; ++t) {
+      dkacc[mt][t] = f32x16{};
+      dvacc[mt][t] = f32x16{};
+      asm volatile("" : "+a"(dkacc[mt][t]), "+a"(dvacc[mt][t]));
+    }
 
   auto row_read = [&](int stg, int tilesel, int ks) {
     return as_vec8<T>(*reinterpret_cast<const u32x4*>(
@@ -429,7 +444,7 @@ __device__ __forceinline__ void dkdv_tile(
   // Every step copies exactly one item (past the last item it re-copies the
   // last one into the free stage), so item i+1 has landed once at most NS-3
   // younger items are in flight.
-  f32x16 sA, pA, sB, pB;
+  f32x16 sA[KTL], pA[KTL], sB[KTL], pB[KTL];
   f32x4 lA[4], dA[4], lB[4], dB[4];
   Copy cpn;
   if (items <= 0) goto epilogue;
@@ -443,12 +458,19 @@ __device__ __forceinline__ void dkdv_tile(
     cpn = copy_of(NS - 1 < items ? NS - 1 : items - 1);
     wait_vmcnt<(NS - 2) * C::PER>();
     __syncthreads();
-    sA = f32x16{};
-    pA = f32x16{};
+#pragma unroll
+    for (int t = 0; t < KTL; ++t) {
+      sA[t] = f32x16{};
+      pA[t] = f32x16{};
+    }
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      sA = E::mfma32(row_read(0, 0, ks), kf[ks], sA);
-      pA = E::mfma32(row_read(0, 1, ks), vf[ks], pA);
+      const V8 qa = row_read(0, 0, ks), da = row_read(0, 1, ks);
+#pragma unroll
+      for (int t = 0; t < KTL; ++t) {
+        sA[t] = E::mfma32(qa, kf[t][ks], sA[t]);
+        pA[t] = E::mfma32(da, vf[t][ks], pA[t]);
+      }
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g) read_stats(0, lA, dA, g);
@@ -459,8 +481,9 @@ __device__ __forceinline__ void dkdv_tile(
     // of A(i+1), then C(i).  LDS operands stream with a lookahead of L: rows
     // of item i+1 for A, then transposed tiles of item i for C, then the
     // statistics of item i+1.  The copy of item i+NS-1 goes to stage S-1.
-    auto step = [&](auto stage_c, int it, f32x16& sc, f32x16& pc, f32x16& sn, f32x16& pn,
-                    f32x4 (&lc)[4], f32x4 (&dc)[4], f32x4 (&ln)[4], f32x4 (&dn)[4]) {
+    auto step = [&](auto stage_c, int it, f32x16 (&sc)[KTL], f32x16 (&pc)[KTL],
+                    f32x16 (&sn)[KTL], f32x16 (&pn)[KTL], f32x4 (&lc)[4], f32x4 (&dc)[4],
+                    f32x4 (&ln)[4], f32x4 (&dn)[4]) {
       constexpr int S = decltype(stage_c)::value;
       constexpr int SN = (S + 1) % NS, SP = (S + NS - 1) % NS;
       wait_vmcnt<(NS - 3) * C::PER>();
@@ -482,51 +505,73 @@ __device__ __forceinline__ void dkdv_tile(
       };
 #pragma unroll
       for (int x = 0; x < L; ++x) issue(x);
-      sn = f32x16{};
-      pn = f32x16{};
-      // B(i) is spread over the NA MFMAs of A(i+1) and the first NC/2 of C(i):
-      // value x at stream position x * (NA + NC/2) / 16, so that about four
-      // VALU operations sit under each MFMA.  Values 0-7 feed the first half of
-      // C and are done inside A; dS trails P by one value (exp latency).
-      float pv[16], dsv[16];
+#pragma unroll
+      for (int t = 0; t < KTL; ++t) {
+        sn[t] = f32x16{};
+        pn[t] = f32x16{};
+      }
+      // B(i) is spread over the NA reads of A(i+1) and the first NC/2 of C(i):
+      // value x at stream position x * (NA + NC/2) / NV, so that about four
+      // VALU operations sit under each MFMA.  Value x is element e of key tile
+      // t, in the order the halves of C consume them (rows 0-7 of every key
+      // tile, then rows 8-15); the first half is done inside A; dS trails P
+      // by one value (exp latency).
+      float pv[KTL][16], dsv[KTL][16];
       auto b_slot = [&](int pos) {
 #pragma unroll
-        for (int x = 0; x < 16; ++x)
-          if (x * (NA + NC / 2) / 16 == pos) {
-            pv[x] = fast_exp2(fmaf(sc[x], c2, -lc[x >> 2][x & 3]));
-            if (x >= 1) dsv[x - 1] = pv[x - 1] * (pc[x - 1] - dc[(x - 1) >> 2][(x - 1) & 3]);
-            if (x == 15) dsv[15] = pv[15] * (pc[15] - dc[3][3]);
+        for (int x = 0; x < NV; ++x)
+          if (x * (NA + NC / 2) / NV == pos) {
+            const int t = (x / 8) % KTL, e = 8 * (x / (8 * KTL)) + x % 8;
+            pv[t][e] = fast_exp2(fmaf(sc[t][e], c2, -lc[e >> 2][e & 3]));
+            if (x >= 1) {
+              const int y = x - 1;
+              const int ty = (y / 8) % KTL, ey = 8 * (y / (8 * KTL)) + y % 8;
+              dsv[ty][ey] = pv[ty][ey] * (pc[ty][ey] - dc[ey >> 2][ey & 3]);
+            }
+            if (x == NV - 1) dsv[t][e] = pv[t][e] * (pc[t][e] - dc[e >> 2][e & 3]);
           }
       };
-      static_assert(8 * (NA + NC / 2) / 16 < NA, "dS 0-7 must be done inside A");
+      static_assert(8 * KTL * (NA + NC / 2) / NV < NA, "the first half of dS must be done inside A");
 #pragma unroll
       for (int u = 0; u < NA; ++u) {
         issue(u + L);
 #pragma unroll
         for (int p = 0; p < C::PER; ++p)
           if ((p * NA) / C::PER == u) copy_piece(cp, SP, p);
-        if (u & 1)
-          pn = E::mfma32(op[u], vf[u >> 1], pn);
-        else
-          sn = E::mfma32(op[u], kf[u >> 1], sn);
+#pragma unroll
+        for (int t = 0; t < KTL; ++t) {
+          if (u & 1)
+            pn[t] = E::mfma32(op[u], vf[t][u >> 1], pn[t]);
+          else
+            sn[t] = E::mfma32(op[u], kf[t][u >> 1], sn[t]);
+        }
         b_slot(u);
         __builtin_amdgcn_sched_barrier(0);
       }
-      V8 bp[2], bs[2];
-      bp[0] = pack8<T>(pv);
-      bs[0] = pack8<T>(dsv);
+      V8 bp[KTL][2], bs[KTL][2];
+#pragma unroll
+      for (int t = 0; t < KTL; ++t) {
+        bp[t][0] = pack8<T>(pv[t]);
+        bs[t][0] = pack8<T>(dsv[t]);
+      }
 #pragma unroll
       for (int vv = 0; vv < NC; ++vv) {
         issue(NA + vv + L);
         const int j = vv / (2 * (C::DH / 32)), mt = (vv >> 1) % (C::DH / 32);
-        if (vv & 1)
-          dkacc[mt] = E::mfma32(op[NA + vv], bs[j], dkacc[mt]);
-        else
-          dvacc[mt] = E::mfma32(op[NA + vv], bp[j], dvacc[mt]);
+#pragma unroll
+        for (int t = 0; t < KTL; ++t) {
+          if (vv & 1)
+            dkacc[mt][t] = E::mfma32(op[NA + vv], bs[t][j], dkacc[mt][t]);
+          else
+            dvacc[mt][t] = E::mfma32(op[NA + vv], bp[t][j], dvacc[mt][t]);
+        }
         if (vv < NC / 2) b_slot(NA + vv);
         if (vv == NC / 2 - 1) {
-          bp[1] = pack8<T>(pv + 8);
-          bs[1] = pack8<T>(dsv + 8);
+#pragma unroll
+          for (int t = 0; t < KTL; ++t) {
+            bp[t][1] = pack8<T>(pv[t] + 8);
+            bs[t][1] = pack8<T>(dsv[t] + 8);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -559,22 +604,16 @@ __device__ __forceinline__ void dkdv_tile(
 
 epilogue:
   // ---- epilogue ------------------------------------------------------------
-  // dK / dV row: this key's slot, or with RASTER its raster row orows[mykey]
-  // in a sequence of s_out tokens (a padding slot, < 0, has none)
-  int64_t otok = ktok;
-  if constexpr (RASTER) {
-    const int r = orows[mykey];
-    otok = (r >= 0 && r < s_out) ? raster_row(b, r, s_out, heads) : -1;
-  }
-  const bool ostore = !RASTER || otok >= 0;
   const float cdiv = (float)(cnt > 1 ? cnt : 1), rcp = 1.0f / cdiv;
   const T* kcrow = dkc ? dkc + ((int64_t)b * kb + kvblk) * D : nullptr;
   const T* vcrow = dvc ? dvc + ((int64_t)b * kb + kvblk) * D : nullptr;
   // The pooled-gradient rows are loaded together before the first store: a
   // load issued after a store waits for that store too (one in-order vector
   // memory counter), which made the epilogue 16 store round trips long.
+  // every key of the wave is in one key block: one pooled row for all of them
+  const bool any_valid = mykey0 - kvblk * BE < nvb;
   u32x2 kcv[C::DH / 32][4], vcv[C::DH / 32][4];
-  if (key_valid && kcrow) {
+  if (any_valid && kcrow) {
 #pragma unroll
     for (int mt = 0; mt < C::DH / 32; ++mt)
 #pragma unroll
@@ -585,33 +624,46 @@ epilogue:
       }
   }
 #pragma unroll
-  for (int mt = 0; mt < C::DH / 32; ++mt) {
+  for (int t = 0; t < KTL; ++t) {
+    const int mykey = mykey0 + 32 * t;
+    const bool key_valid = (mykey - kvblk * BE) < nvb;
+    // dK / dV row: this key's slot, or with RASTER its raster row orows[mykey]
+    // in a sequence of s_out tokens (a padding slot, < 0, has none)
+    int64_t otok = (int64_t)b * skv + mykey;
+    if constexpr (RASTER) {
+      const int r = orows[mykey];
+      otok = (r >= 0 && r < s_out) ? raster_row(b, r, s_out, heads) : -1;
+    }
+    const bool ostore = !RASTER || otok >= 0;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = d_off + mt * 32 + 8 * g + 4 * h;
-      float ck[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (key_valid && kcrow) {
-        const T* ka = reinterpret_cast<const T*>(&kcv[mt][g]);
-        const T* va = reinterpret_cast<const T*>(&vcv[mt][g]);
+    for (int mt = 0; mt < C::DH / 32; ++mt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = d_off + mt * 32 + 8 * g + 4 * h;
+        float ck[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (key_valid && kcrow) {
+          const T* ka = reinterpret_cast<const T*>(&kcv[mt][g]);
+          const T* va = reinterpret_cast<const T*>(&vcv[mt][g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            ck[e] = round_t<T>(div_by_count(E::to_f(ka[e]), cdiv, rcp));
+            cv[e] = round_t<T>(div_by_count(E::to_f(va[e]), cdiv, rcp));
+          }
+        }
+        // A padding key gets no gradient; its lane's accumulators (which only
+        // ever hold that key) are dropped here instead of masking every score.
+        T k4[4], v4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          ck[e] = round_t<T>(div_by_count(E::to_f(ka[e]), cdiv, rcp));
-          cv[e] = round_t<T>(div_by_count(E::to_f(va[e]), cdiv, rcp));
+          const float fk = key_valid ? round_t<T>(dkacc[mt][t][4 * g + e] * scale) : 0.f;
+          const float fv = key_valid ? round_t<T>(dvacc[mt][t][4 * g + e]) : 0.f;
+          k4[e] = E::from_f(fk + ck[e]);
+          v4[e] = E::from_f(fv + cv[e]);
         }
-      }
-      // A padding key gets no gradient; its lane's accumulators (which only
-      // ever hold that key) are dropped here instead of masking every score.
-      T k4[4], v4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float fk = key_valid ? round_t<T>(dkacc[mt][4 * g + e] * scale) : 0.f;
-        const float fv = key_valid ? round_t<T>(dvacc[mt][4 * g + e]) : 0.f;
-        k4[e] = E::from_f(fk + ck[e]);
-        v4[e] = E::from_f(fv + cv[e]);
-      }
-      if (ostore) {
-        *reinterpret_cast<u32x2*>(dk + otok * D + d0) = *reinterpret_cast<const u32x2*>(k4);
-        *reinterpret_cast<u32x2*>(dv + otok * D + d0) = *reinterpret_cast<const u32x2*>(v4);
+        if (ostore) {
+          *reinterpret_cast<u32x2*>(dk + otok * D + d0) = *reinterpret_cast<const u32x2*>(k4);
+          *reinterpret_cast<u32x2*>(dv + otok * D + d0) = *reinterpret_cast<const u32x2*>(v4);
+        }
       }
     }
   }
@@ -1128,11 +1180,12 @@ struct DkvGeometry {
 };
 static bool dkdv_geometry(int D, int be, int64_t skv, DkvGeometry& g) {
   if (!((D == 64 || D == 128 || D == 256) && (be == 64 || be == 128 || be == 256))) return false;
-  const int kt = be >= 128 ? 128 : be;  // DkvCfg<D, BE>::KT
+  const int kw = D == 64 ? 64 : 32;                 // DkvCfg<D, BE>::KW
+  const int kt = be < 4 * kw ? be : 4 * kw;        // DkvCfg<D, BE>::KT
   g.tph = (int)(skv / kt);
   g.tpb = be / kt;
   g.nsplit = D > 128 ? 2 : 1;
-  g.wg_per_cu = 4 / (kt / 32);          // one wave per SIMD
+  g.wg_per_cu = 4 / (kt / kw);                     // one wave per SIMD
   return true;
 }
 

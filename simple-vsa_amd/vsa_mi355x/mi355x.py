@@ -373,7 +373,8 @@ def dkdv_tile_order(counts, bh, skv, head_dim, block_elements):
     range longest-first when one key block's in-edge count would otherwise set
     the kernel's end (skewed routes), else in order, followed by the counters
     the persistent workgroups take tiles from (see vsa_dkdv_tile_order)."""
-    kt = 128 if block_elements >= 128 else block_elements
+    # keys per workgroup: four waves of 64 keys at head_dim 64, of 32 above
+    kt = min(block_elements, 256 if head_dim == 64 else 128)
     tiles = bh * (skv // kt) * (2 if head_dim > 128 else 1)
     order = torch.empty(8 * ((tiles + 7) // 8) + 16, device=counts.device, dtype=torch.int32)
     _lib.call("vsa_dkdv_tile_order", _lib.ptr(counts), _lib.ptr(order), order.numel(), bh, skv,

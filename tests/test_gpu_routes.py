@@ -86,13 +86,15 @@ def _order_case(H, nb, be, D, hot):
 
 
 @pytest.mark.parametrize("H,nb,be,D,hot", [(4, 160, 64, 64, 2), (2, 60, 256, 128, 1),
-                                           (3, 40, 128, 256, 2), (16, 160, 256, 128, 0)])
+                                           (3, 40, 128, 256, 2), (16, 160, 256, 128, 0),
+                                           (3, 48, 256, 64, 1), (2, 64, 128, 64, 0)])
 def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
     from vsa_mi355x import _lib
     M, q, k, v, do, lse, delta, sel, vbs, inv, off, cnt, scale, tk = _order_case(H, nb, be, D, hot)
     S = nb * be
     order = M.dkdv_tile_order(cnt, H, S, D, be)
-    kt = 128 if be >= 128 else be
+    kw = 64 if D == 64 else 32                                # keys per wave
+    kt = min(be, 4 * kw)                                      # keys per workgroup
     nsplit = 2 if D > 128 else 1
     tiles = H * (S // kt) * nsplit
     per = (tiles + 7) // 8
@@ -104,7 +106,7 @@ def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
     assert (o[o >= tiles] == tiles).all()                     # the rest are the sentinel
     nedge = cnt.cpu().reshape(H, nb).repeat_interleave(be // kt, 1).reshape(-1)
     nedge = nedge.repeat_interleave(nsplit)
-    slots = 32 * (4 // (kt // 32))                            # concurrent workgroups per XCD
+    slots = 32 * (4 // (kt // kw))                            # concurrent workgroups per XCD
     sorted_ranges = 0
     for x in range(8):                                        # each XCD keeps its own range
         ids = o[x::8]
