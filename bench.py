@@ -39,6 +39,9 @@ WORKLOADS = {
                block=(1, 1, 256), topk=8, gate="token", last_valid=200),
     "c3": dict(name="Video-DiT mid shape (BASELINE configs[2])", B=1, H=40, S=40960, D=128,
                block=(4, 8, 8), topk=20, gate="full"),
+    # c3 with a per-token gate [B, H, S, 1] (the config leaves the gate's shape open)
+    "c3tok": dict(name="Video-DiT mid shape, gate [B,H,S,1]", B=1, H=40, S=40960, D=128,
+                  block=(4, 8, 8), topk=20, gate="token"),
     "c4": dict(name="Long video shape (BASELINE configs[3])", B=1, H=40, S=92160, D=128,
                block=(1, 1, 256), topk=45, gate=None, every8th=192, amp=0.5),
     "c5": dict(name="Route-skew explicit routing (BASELINE configs[4])", B=1, H=24, S=40960,
@@ -541,7 +544,7 @@ def main():
         del q, k, v, do, gate, qd, kd, vd, gd, out, lse, fine, delta, dq, dk, dv
         torch.cuda.empty_cache()
         workloads = {}
-        for key in ("c2", "c4", "c5"):
+        for key in ("c2", "c3tok", "c4", "c5"):
             r = run_workload(key, args.workload_steps, 2)
             workloads[key] = {n: r[n] for n in ("ms_fwd_bwd", "ms_fwd", "tflops_fwd_bwd",
                                                 "tflops_fwd", "pct_bf16_peak_fwd_bwd",

@@ -13,6 +13,8 @@
  *    no framework types cross this boundary;
  *  - tensors are contiguous row-major; q-like tensors are [BH, Sq, D], k/v-like
  *    [BH, Skv, D], block vectors [BH, nblocks, D], where BH = batch * heads;
+ *    every tensor pointer is 16-byte aligned (rows are read and written with
+ *    16-byte accesses);
  *  - dtype: VSA_BF16, VSA_F16 or VSA_F32 for every kernel (the fine kernels
  *    run bf16 / fp16 on MFMA and fp32 on fp32 kernels, same results contract);
  *  - nothing here allocates or frees device memory: every output and every

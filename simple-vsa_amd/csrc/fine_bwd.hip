@@ -67,32 +67,35 @@ __device__ __forceinline__ void dq_epilogue(const f32x16 (&dqacc)[D / 32], int64
     crow = dqc + ((int64_t)b * qb + qblk) * D;
   }
   const float rcp = 1.0f / cdiv;
-  u32x2 cr[D / 32][4];  // loaded together, so their latency is paid once
+  // the row regrouped for 16-byte accesses: w[mt][p][i] is dim
+  // mt*32 + 8(2p + h) + i (both lanes of a swapped pair hold this query, so
+  // they return above together)
+  float w[D / 32][2][8];
+#pragma unroll
+  for (int mt = 0; mt < D / 32; ++mt) swap_rows16(dqacc[mt], scale, w[mt]);
+  u32x4 cr[D / 32][2];  // loaded together, so their latency is paid once
   if (cvalid) {
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        cr[mt][g] = *reinterpret_cast<const u32x2*>(crow + mt * 32 + 8 * g + 4 * h);
+      for (int p = 0; p < 2; ++p)
+        cr[mt][p] = *reinterpret_cast<const u32x4*>(crow + mt * 32 + 16 * p + 8 * h);
   }
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = mt * 32 + 8 * g + 4 * h;
-      float cval[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < 2; ++p) {
+      const int d0 = mt * 32 + 16 * p + 8 * h;
+      float cval[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       if (cvalid) {
-        const T* cc = reinterpret_cast<const T*>(&cr[mt][g]);
+        const T* cc = reinterpret_cast<const T*>(&cr[mt][p]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) cval[e] = round_t<T>(div_by_count(E::to_f(cc[e]), cdiv, rcp));
+        for (int e = 0; e < 8; ++e) cval[e] = round_t<T>(div_by_count(E::to_f(cc[e]), cdiv, rcp));
       }
-      T o4[4];
+      T o8[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float val = round_t<T>(dqacc[mt][4 * g + e] * scale);
-        o4[e] = E::from_f(val + cval[e]);
-      }
-      *reinterpret_cast<u32x2*>(dq + tok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
+      for (int e = 0; e < 8; ++e) o8[e] = E::from_f(round_t<T>(w[mt][p][e]) + cval[e]);
+      *reinterpret_cast<u32x4*>(dq + tok * D + d0) = *reinterpret_cast<const u32x4*>(o8);
     }
   }
 }
@@ -612,15 +615,18 @@ epilogue:
   // memory counter), which made the epilogue 16 store round trips long.
   // every key of the wave is in one key block: one pooled row for all of them
   const bool any_valid = mykey0 - kvblk * BE < nvb;
-  u32x2 kcv[C::DH / 32][4], vcv[C::DH / 32][4];
+  // rows regrouped for 16-byte accesses (swap_rows16): w[p][i] is dim
+  // d_off + mt*32 + 8(2p + h) + i of this lane's key; both lanes of a swapped
+  // pair hold the same key
+  u32x4 kcv[C::DH / 32][2], vcv[C::DH / 32][2];
   if (any_valid && kcrow) {
 #pragma unroll
     for (int mt = 0; mt < C::DH / 32; ++mt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = d_off + mt * 32 + 8 * g + 4 * h;
-        kcv[mt][g] = *reinterpret_cast<const u32x2*>(kcrow + d0);
-        vcv[mt][g] = *reinterpret_cast<const u32x2*>(vcrow + d0);
+      for (int p = 0; p < 2; ++p) {
+        const int d0 = d_off + mt * 32 + 16 * p + 8 * h;
+        kcv[mt][p] = *reinterpret_cast<const u32x4*>(kcrow + d0);
+        vcv[mt][p] = *reinterpret_cast<const u32x4*>(vcrow + d0);
       }
   }
 #pragma unroll
@@ -637,32 +643,36 @@ epilogue:
     const bool ostore = !RASTER || otok >= 0;
 #pragma unroll
     for (int mt = 0; mt < C::DH / 32; ++mt) {
+      float wk[2][8], wv[2][8];
+      swap_rows16(dkacc[mt][t], scale, wk);
+      swap_rows16(dvacc[mt][t], 1.0f, wv);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = d_off + mt * 32 + 8 * g + 4 * h;
-        float ck[4] = {0.f, 0.f, 0.f, 0.f}, cv[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < 2; ++p) {
+        const int d0 = d_off + mt * 32 + 16 * p + 8 * h;
+        float ck[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float cv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (key_valid && kcrow) {
-          const T* ka = reinterpret_cast<const T*>(&kcv[mt][g]);
-          const T* va = reinterpret_cast<const T*>(&vcv[mt][g]);
+          const T* ka = reinterpret_cast<const T*>(&kcv[mt][p]);
+          const T* va = reinterpret_cast<const T*>(&vcv[mt][p]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
+          for (int e = 0; e < 8; ++e) {
             ck[e] = round_t<T>(div_by_count(E::to_f(ka[e]), cdiv, rcp));
             cv[e] = round_t<T>(div_by_count(E::to_f(va[e]), cdiv, rcp));
           }
         }
         // A padding key gets no gradient; its lane's accumulators (which only
         // ever hold that key) are dropped here instead of masking every score.
-        T k4[4], v4[4];
+        T k8[8], v8[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float fk = key_valid ? round_t<T>(dkacc[mt][t][4 * g + e] * scale) : 0.f;
-          const float fv = key_valid ? round_t<T>(dvacc[mt][t][4 * g + e]) : 0.f;
-          k4[e] = E::from_f(fk + ck[e]);
-          v4[e] = E::from_f(fv + cv[e]);
+        for (int e = 0; e < 8; ++e) {
+          const float fk = key_valid ? round_t<T>(wk[p][e]) : 0.f;
+          const float fv = key_valid ? round_t<T>(wv[p][e]) : 0.f;
+          k8[e] = E::from_f(fk + ck[e]);
+          v8[e] = E::from_f(fv + cv[e]);
         }
         if (ostore) {
-          *reinterpret_cast<u32x2*>(dk + otok * D + d0) = *reinterpret_cast<const u32x2*>(k4);
-          *reinterpret_cast<u32x2*>(dv + otok * D + d0) = *reinterpret_cast<const u32x2*>(v4);
+          *reinterpret_cast<u32x4*>(dk + otok * D + d0) = *reinterpret_cast<const u32x4*>(k8);
+          *reinterpret_cast<u32x4*>(dv + otok * D + d0) = *reinterpret_cast<const u32x4*>(v8);
         }
       }
     }
@@ -1020,7 +1030,10 @@ sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
     if (tile >= num_tiles) break;
     dq_pp_tile<T, D, RASTER>(smem, tile, q, k, v, dout, lse, delta, selected, kv_vbs, dq, dqc,
                              q_vbs, sq, skv, qb, kb, topk, c2, qsign, scale, orows, s_out, heads);
-    dma_wait();
+    // No copy is in flight here (each chunk's copies are waited for before it
+    // is read, and past the route's end nothing is copied): only the
+    // epilogue's stores are outstanding, and they drain under the next tile's
+    // first loads.
     __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
   }
 }

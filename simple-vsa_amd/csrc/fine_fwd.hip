@@ -76,57 +76,57 @@ __device__ __forceinline__ void fwd_epilogue(const f32x16 (&oacc)[D / 32], float
   if (gate_mode == 1 && ostore) grow = gate + otok * D;
   if (!RASTER && gate_mode == 3)
     grow = gate + (((int64_t)(b / gate_heads) * sq + myq) * gate_heads + b % gate_heads) * D;
-  // the combine operands are loaded together, so their latency is paid once
-  u32x2 ocr[D / 32][4], gr[D / 32][4];
+  // The row regrouped so that every global access below is 16 bytes wide (half
+  // the memory instructions of the accumulator's 8-byte pieces): after
+  // swap_rows16, w[p][i] is dim mt*32 + 8(2p + h) + i.  The combine operands
+  // are loaded first, together, so their latency is paid once.
+  u32x4 ocr[D / 32][2], gr[D / 32][2];
   if (ocrow) {
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        ocr[mt][g] = *reinterpret_cast<const u32x2*>(ocrow + mt * 32 + 8 * g + 4 * h);
+      for (int p = 0; p < 2; ++p)
+        ocr[mt][p] = *reinterpret_cast<const u32x4*>(ocrow + mt * 32 + 16 * p + 8 * h);
   }
   if (grow) {
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        gr[mt][g] = *reinterpret_cast<const u32x2*>(grow + mt * 32 + 8 * g + 4 * h);
+      for (int p = 0; p < 2; ++p)
+        gr[mt][p] = *reinterpret_cast<const u32x4*>(grow + mt * 32 + 16 * p + 8 * h);
   }
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) {
+    float w[2][8];
+    swap_rows16(oacc[mt], inv, w);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = mt * 32 + 8 * g + 4 * h;
-      float val[4];
+    for (int p = 0; p < 2; ++p) {
+      const int d0 = mt * 32 + 16 * p + 8 * h;
+      float val[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) val[e] = oacc[mt][4 * g + e] * inv;
+      for (int e = 0; e < 8; ++e) val[e] = w[p][e];
       if (ocrow) {
-        const T* oc = reinterpret_cast<const T*>(&ocr[mt][g]);
-        float gv[4] = {gtok, gtok, gtok, gtok};
-        if (grow) {
-          const T* gg = reinterpret_cast<const T*>(&gr[mt][g]);
+        const T* oc = reinterpret_cast<const T*>(&ocr[mt][p]);
+        float gv[8];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) gv[e] = E::to_f(gg[e]);
+        for (int e = 0; e < 8; ++e) gv[e] = gtok;
+        if (grow) {
+          const T* gg = reinterpret_cast<const T*>(&gr[mt][p]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) gv[e] = E::to_f(gg[e]);
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) val[e] = fmaf(E::to_f(oc[e]), gv[e], val[e]);
+        for (int e = 0; e < 8; ++e) val[e] = fmaf(E::to_f(oc[e]), gv[e], val[e]);
       }
-      T o4[4];
+      T o8[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = E::from_f(val[e]);
-      if (ostore) *reinterpret_cast<u32x2*>(out + otok * D + d0) = *reinterpret_cast<const u32x2*>(o4);
-    }
-  }
-  if (ocrow && fine) {  // the fine output as stored in T, for the backward's delta
+      for (int e = 0; e < 8; ++e) o8[e] = E::from_f(val[e]);
+      if (ostore) *reinterpret_cast<u32x4*>(out + otok * D + d0) = *reinterpret_cast<const u32x4*>(o8);
+      if (ocrow && fine) {  // the fine output as stored in T, for the backward's delta
+        T f8[8];
 #pragma unroll
-    for (int mt = 0; mt < D / 32; ++mt) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        T f4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) f4[e] = E::from_f(oacc[mt][4 * g + e] * inv);
-        *reinterpret_cast<u32x2*>(fine + tok * D + mt * 32 + 8 * g + 4 * h) =
-            *reinterpret_cast<const u32x2*>(f4);
+        for (int e = 0; e < 8; ++e) f8[e] = E::from_f(w[p][e]);
+        *reinterpret_cast<u32x4*>(fine + tok * D + d0) = *reinterpret_cast<const u32x4*>(f8);
       }
     }
   }
@@ -647,7 +647,10 @@ sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
     if (tile >= num_tiles) break;
     fwd_pp_tile<T, D, RASTER>(smem, tile, q, k, v, selected, kv_vbs, out, fine, lse, outc, gate,
                               gate_mode, gate_heads, sq, skv, qb, kb, topk, c2, qsign, orows, s_out, heads);
-    dma_wait();
+    // No copy is in flight here (every chunk's copy is waited for before the
+    // chunk is read, and past the route's end nothing is copied), so only the
+    // epilogue's stores are outstanding: they drain under the next tile's
+    // first loads instead of in front of them.
     __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
   }
 }

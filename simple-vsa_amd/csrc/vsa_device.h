@@ -379,6 +379,25 @@ __device__ __forceinline__ float pair_sum32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// One 32x32 MFMA accumulator tile whose rows are 32 dims of the rows (query or
+// key) r = lane & 31: lane (r, h = lane >> 5) holds element 4g + e = dim
+// 8g + 4h + e, g < 4, e < 4.  Regrouped for 16-byte accesses: one
+// v_permlane32_swap per value of the pairs g = (2p, 2p + 1) leaves lane h with
+// the eight consecutive dims 8(2p + h) + i in w[p][i] (each value times mul).
+// Both lanes of a pair must be active.
+__device__ __forceinline__ void swap_rows16(const f32x16& acc, float mul, float (&w)[2][8]) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[8 * p + e] * mul),
+                                                       __float_as_uint(acc[8 * p + 4 + e] * mul),
+                                                       false, false);
+      w[p][e] = __uint_as_float(sw[0]);
+      w[p][4 + e] = __uint_as_float(sw[1]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Wave / block reductions (wave64)
 // ---------------------------------------------------------------------------

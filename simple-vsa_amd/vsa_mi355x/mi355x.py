@@ -193,6 +193,15 @@ def _padded(q, k, be):
     return kbe, kd, pad_q, pad_k, unpad_out
 
 
+def _aligned16(x: Optional[Tensor]) -> Optional[Tensor]:
+    """x itself when its data is 16-byte aligned (the kernels read and write
+    rows with 16-byte accesses), else a copy with the same strides (a view with
+    an odd storage offset)."""
+    if x is None or x.data_ptr() % 16 == 0:
+        return x
+    return x.clone()
+
+
 def _i32(x: Tensor, device) -> Tensor:
     return x.to(device=device, dtype=torch.int32).contiguous()
 
@@ -398,7 +407,7 @@ class _SparseAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         q, k, v, out, lse, selected, vbs = ctx.saved_tensors
-        dout = dout.contiguous()
+        dout = _aligned16(dout.contiguous())
         delta, _, _ = backward_prep(out, dout, ctx.block_elements)
         dq, dk, dv = sparse_backward(q, k, v, dout, lse, delta, selected, vbs,
                                      ctx.block_elements, ctx.scale)
@@ -438,7 +447,7 @@ def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
                                           variable_block_sizes, block_size=(1, 1, kbe),
                                           sm_scale=scale)
             return unpad_out(out)
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q, k, v = (_aligned16(x.contiguous()) for x in (q, k, v))
     selected = _i32(selected, q.device)
     vbs = _i32(variable_block_sizes, q.device)
     with torch.cuda.device(q.device):
@@ -480,7 +489,7 @@ class _VSA(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, fine, lse = ctx.saved_tensors
-        dout = dout.contiguous()
+        dout = _aligned16(dout.contiguous())
         delta, d_outc, d_gate = backward_prep(fine, dout, ctx.be, out_c=outc, gate=gate)
         dqc, dkc, dvc = coarse_backward(qc, kc, vc, probs, d_outc, ctx.scale)
         dq, dk, dv = sparse_backward(q, k, v, dout, lse, delta, sel, vbs, ctx.be, ctx.scale,
@@ -534,7 +543,8 @@ def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
     be = as_block_elements(block_size)
     validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
     _check_device_path(q, k, v, be)
-    gate = _prepare_gate(compress_attn_weight, q)
+    gate = _aligned16(_prepare_gate(compress_attn_weight, q))
+    q, k, v = (_aligned16(x) for x in (q, k, v))
     scale = 1.0 / math.sqrt(q.shape[-1])
     vbs = _i32(variable_block_sizes, q.device)
     qvbs = _i32(q_variable_block_sizes, q.device)

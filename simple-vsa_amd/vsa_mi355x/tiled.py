@@ -116,7 +116,7 @@ class _VSATiled(torch.autograd.Function):
         shape, (b, h, s_out, d), nb, be, scale, token_major = ctx.dims
         heads = h if token_major else 0
         L = nb * be
-        dout = dout.contiguous()
+        dout = M._aligned16(dout.contiguous())
         code, stream = _lib.dtype_code(dout.dtype), _lib.stream_of(dout)
         delta = torch.empty((b, h, L), device=dout.device, dtype=torch.float32)
         d_outc = torch.empty_like(outc)
@@ -249,9 +249,9 @@ def mi355x_vsa_tiled(q: Tensor, k: Tensor, v: Tensor, dit_seq_shape: Tuple[int, 
             return _composition(q, k, v, meta, nb, be, ts, topk, gate, token_major)
         vbs = meta["variable_block_sizes"].to(torch.int32)
         rows = slot_rows(shape, ts, q.device)
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        q, k, v = (M._aligned16(x.contiguous()) for x in (q, k, v))
         if gate is not None:
-            gate = gate.contiguous()
+            gate = M._aligned16(gate.contiguous())
         scale = 1.0 / math.sqrt(d)
         needs_grad = torch.is_grad_enabled() and (
             q.requires_grad or k.requires_grad or v.requires_grad

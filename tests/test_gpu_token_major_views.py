@@ -144,3 +144,33 @@ def test_views_without_a_raster_kernel_take_the_contiguous_path():
     assert torch.equal(M.mi355x_vsa(q, k, v, vbs, qvbs, 2, blk),
                        M.mi355x_vsa(q.contiguous(), k.contiguous(), v.contiguous(), vbs, qvbs,
                                     2, blk))
+
+
+def test_inputs_off_16_byte_alignment_give_the_same_result():
+    """q, k, v, gate and dout whose data starts 2 bytes past a 16-byte boundary
+    (contiguous views with an odd storage offset): the host copies them before
+    the kernels, whose rows are read and written 16 bytes at a time."""
+    from vsa_mi355x import mi355x as M
+    b, h, nb, d, be = 1, 3, 4, 128, 64
+    s = nb * be
+    g = torch.Generator().manual_seed(23)
+    vbs = _counts(nb, be, g)
+
+    def odd(x):
+        buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=DEV)
+        y = buf[1:].view(x.shape)
+        y.copy_(x)
+        assert y.data_ptr() % 16 != 0
+        return y
+
+    src = [torch.randn(b, h, s, d, generator=g).to(torch.bfloat16).to(DEV) for _ in range(4)]
+    gate = (2.0 * torch.rand(b, h, s, d, generator=g)).to(torch.bfloat16).to(DEV)
+    res = []
+    for make in (lambda x: x.clone(), odd):
+        leaves = [make(x).requires_grad_() for x in src[:3]]
+        gl = make(gate).requires_grad_()
+        out = M.mi355x_vsa(*leaves, vbs, vbs, 2, (1, 1, be), gl)
+        out.backward(make(src[3]))
+        res.append([out.detach()] + [x.grad for x in leaves] + [gl.grad])
+    for name, a, b_ in zip(["out", "dq", "dk", "dv", "dgate"], *res):
+        assert torch.equal(a, b_), name
