@@ -44,8 +44,20 @@ def _check(a, e, what, max_abs=2e-2, rel_l2=1e-2):
 
 @pytest.mark.parametrize("block,D,nb,topk,gate_kind", CASES)
 def test_padded_shapes_match_oracle(block, D, nb, topk, gate_kind):
+    _full_op_case(block, D, nb, topk, gate_kind)
+
+
+# An int block_size is the edge of a cube of tokens (tests/test_torch_vsa.py:59-72):
+# 2 -> 8 tokens (with head_dim 8, as there), 4 -> 64 (a kernel of its own), 5 -> 125.
+@pytest.mark.parametrize("block,D,nb,topk,gate_kind", [(2, 8, 3, 2, None), (4, 64, 6, 3, "full"),
+                                                       (5, 32, 4, 2, "token")])
+def test_int_block_size_is_a_cube(block, D, nb, topk, gate_kind):
+    _full_op_case(block, D, nb, topk, gate_kind)
+
+
+def _full_op_case(block, D, nb, topk, gate_kind):
     from vsa_mi355x import mi355x as M
-    be = math.prod(block)
+    be = M.as_block_elements(block)
     B, H, S = 1, 2, be * nb
     g = torch.Generator(device=DEV).manual_seed(be * 1000 + D)
     q, k, v, do = (torch.randn(B, H, S, D, generator=g, device=DEV, dtype=torch.bfloat16)
