@@ -202,6 +202,17 @@ def _aligned16(x: Optional[Tensor]) -> Optional[Tensor]:
     return x.clone()
 
 
+def _empty_batch(q: Tensor, *others: Optional[Tensor]) -> Tensor:
+    """The op on an empty batch (batch or heads 0): an empty output of q's shape
+    that is still in the autograd graph of every input (their gradients are
+    empty too), as torch_vsa gives one.  Nothing is launched."""
+    out = q * 0
+    for x in others:
+        if x is not None:
+            out = out + x.sum() * 0
+    return out
+
+
 def _i32(x: Tensor, device) -> Tensor:
     return x.to(device=device, dtype=torch.int32).contiguous()
 
@@ -438,6 +449,8 @@ def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
         raise ValueError("q, k, and v must have shape [batch, heads, seq_len, dim]")
     _check_device_path(q, k, v, be)
     _validate_route(q, k, selected, variable_block_sizes, be)
+    if q.shape[0] * q.shape[1] == 0:
+        return _empty_batch(q, k, v)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     pads = _padded(q, k, be)
     if pads is not None:
@@ -543,6 +556,9 @@ def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
     be = as_block_elements(block_size)
     validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
     _check_device_path(q, k, v, be)
+    if q.shape[0] * q.shape[1] == 0:
+        _prepare_gate(compress_attn_weight, q)  # the same shape checks
+        return _empty_batch(q, k, v, compress_attn_weight)
     gate = _aligned16(_prepare_gate(compress_attn_weight, q))
     q, k, v = (_aligned16(x) for x in (q, k, v))
     scale = 1.0 / math.sqrt(q.shape[-1])

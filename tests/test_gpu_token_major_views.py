@@ -174,3 +174,24 @@ def test_inputs_off_16_byte_alignment_give_the_same_result():
         res.append([out.detach()] + [x.grad for x in leaves] + [gl.grad])
     for name, a, b_ in zip(["out", "dq", "dk", "dv", "dgate"], *res):
         assert torch.equal(a, b_), name
+
+
+@pytest.mark.parametrize("shape", [(0, 3, 256, 64), (2, 0, 256, 64)])
+def test_empty_batch_gives_an_empty_differentiable_output(shape):
+    """batch or heads 0: an empty output of q's shape and empty gradients, as
+    torch_vsa returns, for the full op, the explicit-route op and the tiled op."""
+    from vsa_mi355x import mi355x as M, tiled
+    b, h, s, d = shape
+    vbs = torch.full((s // 64,), 64, dtype=torch.int32, device=DEV)
+    leaves = [torch.randn(*shape, device=DEV, dtype=torch.bfloat16).requires_grad_()
+              for _ in range(3)]
+    gate = torch.rand(*shape, device=DEV, dtype=torch.bfloat16).requires_grad_()
+    sel = torch.zeros(b, h, s // 64, 2, dtype=torch.int32, device=DEV)
+    for out, wrt in ((M.mi355x_vsa(*leaves, vbs, vbs, 2, (1, 1, 64), gate), leaves + [gate]),
+                     (M.mi355x_sparse_attention(*leaves, sel, vbs, block_size=(1, 1, 64)),
+                      leaves),
+                     (tiled.mi355x_vsa_tiled(*leaves, (1, 4, 64), 2, (1, 1, 64), gate),
+                      leaves + [gate])):
+        assert out.shape == shape and out.dtype == torch.bfloat16
+        grads = torch.autograd.grad(out, wrt, torch.ones_like(out))
+        assert all(g_.shape == x.shape for g_, x in zip(grads, wrt))
