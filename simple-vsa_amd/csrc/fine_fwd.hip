@@ -231,8 +231,14 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
       for (int i = 0; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], sacc[smt][i]);
     float smax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
     smax = pair_max32(smax) * c2;
-    if (__any(smax > m + kRescaleSlack)) {
-      const float mnew = fmaxf(m, smax);
+    // Only the lanes whose own chunk max passed the slack move their max (the
+    // branch is wave-uniform, the update is not): a row's values then never
+    // depend on the other rows of its wave, padding rows included.  A lane
+    // that keeps m scales by exp2(0), exactly 1 (m is finite after the first
+    // chunk, where every lane moves).
+    const bool grow = smax > m + kRescaleSlack;
+    if (__any(grow)) {
+      const float mnew = grow ? smax : m;
       const float alpha = fast_exp2(m - mnew);
       lsum *= alpha;
 #pragma unroll
@@ -455,9 +461,11 @@ __device__ __forceinline__ void fwd_pp_tile(
     if (st == 3) {
       float smax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
       smax = pair_max32(smax) * c2;
-      resc = __any(smax > m + kRescaleSlack);
-      const float mnew = resc ? fmaxf(m, smax) : m;
-      alpha = fast_exp2(m - mnew);  // used only when resc
+      // per-lane update under a wave-uniform branch, as in sparse_fwd_kernel
+      const bool grow = smax > m + kRescaleSlack;
+      resc = __any(grow);
+      const float mnew = grow ? smax : m;
+      alpha = fast_exp2(m - mnew);  // used only when resc (1 where m stays)
       m = mnew;
     }
     if (st >= 4) {
