@@ -232,22 +232,27 @@ __device__ __forceinline__ int unswz_row_chunk<64>(int P, int& c) {
 // flight it puts vmcnt(0) in front of later LDS reads it cannot disambiguate
 // (the transpose reads), which would drain the prefetch.  Every consumer of
 // the copied tile waits on vmcnt explicitly (dma_wait) before its barrier.
+// An LDS DMA that follows an SALU write of M0 needs one wait state (GFX9
+// hazard; the compiler inserts it for the copies it issues itself, not inside
+// an asm statement), hence the s_nop 0.  M0 is reserved to the compiler, which
+// sets it before each of its own uses, so it is not listed as clobbered.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+               "s"(lds)
                : "memory");
 }
 
 // Same with 4 bytes per lane (LDS byte address lds + 4*i).
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds)
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds)
                : "memory");
 }
 
 // Same as dma16 with a scalar 64-bit base and a 32-bit per-lane byte offset
 // (saddr form: no per-lane 64-bit address arithmetic).
 __device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
-               "s"(lds)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff),
+               "s"(sbase), "s"(lds)
                : "memory");
 }
 
