@@ -132,3 +132,42 @@ def test_poisoned_padding_leaves_the_explicit_route_unchanged():
         assert torch.isfinite(a.float()).all(), name
         assert torch.equal(torch.where(krows, a, 0), torch.where(krows, e, 0)), name
         assert not torch.where(krows, 0, a).any(), f"{name} of padding keys"
+
+
+@pytest.mark.parametrize("h,nb,be", [(4, 5, 64), (32, 8, 256)])
+def test_poisoned_padding_leaves_token_major_views_unchanged(h, nb, be):
+    """The same check on per-head views of token-major [B, S, H, D] tensors,
+    which run the kernels' raster instantiations."""
+    from vsa_mi355x import mi355x as M
+    b, d, topk = 1, 128, 2
+    g = torch.Generator(device=DEV).manual_seed(h + nb)
+    s = nb * be
+    vbs = torch.full((nb,), be, dtype=torch.int32)
+    vbs[1], vbs[-1] = be // 2 + 3, 5
+    qvbs = vbs.roll(1)
+    kvalid, qvalid = _valid(vbs, be), _valid(qvbs, be)
+    # [B, S, H, D] with the padding tokens zeroed (clean) or poisoned (dirty)
+    tok = [torch.randn(b, s, h, d, generator=g, device=DEV).to(torch.bfloat16) for _ in range(3)]
+    masks = [qvalid, kvalid, kvalid]
+    clean_tm = [torch.where(m.view(1, -1, 1, 1), x, 0) for x, m in zip(tok, masks)]
+    dirty_tm = [_poison(x.transpose(1, 2), m, g).transpose(1, 2).contiguous()
+                for x, m in zip(clean_tm, masks)]
+    do = torch.randn(b, h, s, d, generator=g, device=DEV).to(torch.bfloat16)
+    do = torch.where(qvalid.view(1, 1, -1, 1), do, 0)
+
+    def run(tensors):
+        leaves = [x.detach().clone().requires_grad_() for x in tensors]
+        views = [x.transpose(1, 2) for x in leaves]
+        assert M._raster_views(*views, None, be)
+        out = M.mi355x_vsa(*views, vbs, qvbs, topk, (1, 1, be))
+        grads = torch.autograd.grad(out, leaves, do)
+        return [out.detach()] + [gr.transpose(1, 2) for gr in grads]
+
+    clean, dirty = run(clean_tm), run(dirty_tm)
+    qrows, krows = qvalid.view(1, 1, -1, 1), kvalid.view(1, 1, -1, 1)
+    for name, a, e, rows in zip(["out", "dq", "dk", "dv"], dirty, clean,
+                                [qrows, qrows, krows, krows]):
+        assert torch.isfinite(a.float()).all(), name
+        assert torch.equal(torch.where(rows, a, 0), torch.where(rows, e, 0)), name
+    for name, a in zip(["dk", "dv"], dirty[2:4]):
+        assert not torch.where(krows, 0, a).any(), f"{name} of padding keys"
