@@ -13,8 +13,12 @@
  *    no framework types cross this boundary;
  *  - tensors are contiguous row-major; q-like tensors are [BH, Sq, D], k/v-like
  *    [BH, Skv, D], block vectors [BH, nblocks, D], where BH = batch * heads;
- *    every tensor pointer is 16-byte aligned (rows are read and written with
- *    16-byte accesses);
+ *    tensors of the element type (rows are read and written with 16-byte
+ *    accesses) and the fp32 coarse score / probability buffers start 16-byte
+ *    aligned, int64 index arrays 8-byte, int32 arrays and the per-row fp32
+ *    vectors (lse, delta) 4-byte aligned (the row-move entry points take
+ *    their rows at any alignment); an entry point returns VSA_ERR_ALIGN
+ *    before any launch otherwise;
  *  - dtype: VSA_BF16, VSA_F16 or VSA_F32 for every kernel (the fine kernels
  *    run bf16 / fp16 on MFMA and fp32 on fp32 kernels, same results contract);
  *  - nothing here allocates or frees device memory: every output and every
@@ -60,7 +64,8 @@ enum vsa_status {
   VSA_ERR_DTYPE = -3,       /* dtype not supported by this entry point */
   VSA_ERR_UNSUPPORTED = -4, /* (block_elements, head_dim) pair has no kernel */
   VSA_ERR_LAUNCH = -5,      /* the HIP launch itself failed */
-  VSA_ERR_TOO_LARGE = -6    /* beyond the static scratch of a no-allocation entry point */
+  VSA_ERR_TOO_LARGE = -6,   /* beyond the static scratch of a no-allocation entry point */
+  VSA_ERR_ALIGN = -7        /* a pointer is not aligned as the shared rules require */
 };
 
 /* Text for a status code (static storage). */

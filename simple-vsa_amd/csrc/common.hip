@@ -607,6 +607,9 @@ extern "C" const char* vsa_status_string(int status) {
     case VSA_ERR_LAUNCH: return "HIP kernel launch failed";
     case VSA_ERR_TOO_LARGE:
       return "the sizes need more than the library's static scratch (no-allocation entry point)";
+    case VSA_ERR_ALIGN:
+      return "a pointer is misaligned (16 bytes for element-type and score tensors, 4 for int32 "
+             "arrays and lse / delta)";
     default: return "unknown status";
   }
 }
@@ -625,6 +628,8 @@ extern "C" int vsa_pool_qkv(const void* q, const void* k, const void* v, const i
                             int64_t sq, int64_t skv, int32_t D, int32_t be, int32_t dtype,
                             void* stream) {
   if (!q || !k || !v || !q_vbs || !kv_vbs || !q_c || !k_c || !v_c) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, q_c, k_c, v_c) || !vsa_aligned<4>(q_vbs, kv_vbs))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || be <= 0 || sq <= 0 || skv <= 0 || sq % be || skv % be || !vec_dim_ok(D, dtype))
     return VSA_ERR_SHAPE;
   const int qb = (int)(sq / be), kb = (int)(skv / be);
@@ -647,6 +652,9 @@ extern "C" int vsa_tile_pool_qkv(const void* q, const void* k, const void* v,
   if (!q || !k || !v || !slot_rows || !q_vbs || !kv_vbs || !q_t || !k_t || !v_t || !q_c ||
       !k_c || !v_c)
     return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, q_t, k_t, v_t, q_c, k_c, v_c) ||
+      !vsa_aligned<4>(slot_rows, q_vbs, kv_vbs))
+    return VSA_ERR_ALIGN;
   if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (bh <= 0 || nb <= 0 || be <= 0 || be > 256 || s_out <= 0 || s_out > (int64_t)nb * be ||
       !vec_dim_ok(D, dtype))
@@ -668,6 +676,8 @@ extern "C" int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
                               int32_t qb, int32_t kb, int32_t D, int32_t topk, float scale,
                               int32_t dtype, void* stream) {
   if (!q_c || !k_c || !v_c || !scores || !probs || !out_c) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q_c, k_c, v_c, scores, probs, out_c) || !vsa_aligned<4>(selected))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   if (selected && (topk < 1 || topk > kb)) return VSA_ERR_SHAPE;
@@ -692,6 +702,7 @@ extern "C" int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
 extern "C" int vsa_topk(const float* scores, int32_t* selected, int64_t rows, int32_t kb,
                         int32_t topk, void* stream) {
   if (!scores || !selected) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(scores) || !vsa_aligned<4>(selected)) return VSA_ERR_ALIGN;
   if (rows <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || topk < 1 || topk > kb) return VSA_ERR_SHAPE;
   return topk_radix(scores, selected, rows, kb, topk, (hipStream_t)stream);
 }
@@ -702,6 +713,7 @@ extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* 
                              int32_t* inverse, int64_t bh, int32_t qb, int32_t kb, int32_t topk,
                              void* stream) {
   if (!selected || !counts || !offsets || !inverse) return VSA_ERR_NULL;
+  if (!vsa_aligned<4>(selected, counts, offsets, inverse)) return VSA_ERR_ALIGN;
   if (bh <= 0 || qb <= 0 || kb <= 0 || topk <= 0 || kb > kMaxCsrBlocks || qb > kMaxCsrBlocks ||
       (int64_t)qb * topk > (1 << 30))
     return VSA_ERR_SHAPE;
@@ -721,6 +733,8 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
                             float* delta, void* d_out_c, void* d_gate, int64_t bh, int64_t sq,
                             int32_t D, int32_t be, int32_t dtype, void* stream) {
   if (!fine_out || !dout || !delta) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(fine_out, dout, out_c, gate, d_out_c, d_gate) || !vsa_aligned<4>(delta))
+    return VSA_ERR_ALIGN;
   const bool gate_f32 = (gate_mode & VSA_GATE_F32) != 0;
   gate_mode &= ~VSA_GATE_F32;
   if (gate_mode < 0 || gate_mode > 3 || (gate_f32 && gate_mode == 0)) return VSA_ERR_SHAPE;
@@ -751,6 +765,9 @@ extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const 
                                   void* d_gate, void* dout_t, int64_t bh, int64_t sq, int32_t D,
                                   int32_t be, int32_t dtype, void* stream) {
   if (!fine_out || !dout || !delta || !slot_rows || !dout_t) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(fine_out, dout, out_c, gate, d_out_c, d_gate, dout_t) ||
+      !vsa_aligned<4>(delta, slot_rows))
+    return VSA_ERR_ALIGN;
   if (heads < 0 || (heads > 0 && bh % heads)) return VSA_ERR_SHAPE;
   if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;  // no token-major / fp32 gate here
   if (out_c && !d_out_c) return VSA_ERR_NULL;
@@ -791,6 +808,8 @@ extern "C" int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c,
                               int32_t D, float scale, int32_t dtype, void* stream) {
   if (!q_c || !k_c || !v_c || !probs || !d_out_c || !ds || !d_q_c || !d_k_c || !d_v_c)
     return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q_c, k_c, v_c, probs, d_out_c, ds, d_q_c, d_k_c, d_v_c))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;

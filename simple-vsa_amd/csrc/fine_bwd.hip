@@ -1217,6 +1217,8 @@ extern "C" int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, co
                                  void* stream) {
   if (!q || !k || !v || !dout || !lse || !delta || !selected || !kv_vbs || !dq) return VSA_ERR_NULL;
   if (d_q_c && !q_vbs) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, dout, dq, d_q_c) || !vsa_aligned<4>(lse, delta, selected, kv_vbs, q_vbs))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
@@ -1249,6 +1251,7 @@ extern "C" int vsa_dkdv_tile_order(const int32_t* counts, int32_t* tile_order,
                                    int64_t order_len, int64_t bh, int64_t skv, int32_t D,
                                    int32_t be, void* stream) {
   if (!counts || !tile_order) return VSA_ERR_NULL;
+  if (!vsa_aligned<4>(counts, tile_order)) return VSA_ERR_ALIGN;
   DkvGeometry g;
   if (bh <= 0 || skv <= 0 || be <= 0 || skv % be) return VSA_ERR_SHAPE;
   if (!dkdv_geometry(D, be, skv, g)) return VSA_ERR_UNSUPPORTED;
@@ -1273,6 +1276,9 @@ extern "C" int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v,
       !dk || !dv)
     return VSA_ERR_NULL;
   if ((d_k_c == nullptr) != (d_v_c == nullptr)) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, dout, dk, dv, d_k_c, d_v_c) ||
+      !vsa_aligned<4>(lse, delta, counts, offsets, inverse, kv_vbs, tile_order))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
@@ -1338,6 +1344,9 @@ extern "C" int vsa_sparse_bwd_dkdv_noalloc(const void* q, const void* k, const v
       !dk || !dv)
     return VSA_ERR_NULL;
   if ((d_k_c == nullptr) != (d_v_c == nullptr)) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, dout, dk, dv, d_k_c, d_v_c) ||
+      !vsa_aligned<4>(lse, delta, counts, offsets, inverse, kv_vbs))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
@@ -1377,6 +1386,9 @@ extern "C" int vsa_sparse_bwd_dq_tiled(const void* q, const void* k, const void*
   if (!q || !k || !v || !dout || !lse || !delta || !selected || !kv_vbs || !dq || !slot_rows)
     return VSA_ERR_NULL;
   if (d_q_c && !q_vbs) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, dout, dq, d_q_c) ||
+      !vsa_aligned<4>(lse, delta, selected, kv_vbs, q_vbs, slot_rows))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       s_out <= 0 || s_out > sq || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;
@@ -1409,6 +1421,9 @@ extern "C" int vsa_sparse_bwd_dkdv_tiled(const void* q, const void* k, const voi
       !dk || !dv || !slot_rows)
     return VSA_ERR_NULL;
   if ((d_k_c == nullptr) != (d_v_c == nullptr)) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, dout, dk, dv, d_k_c, d_v_c) ||
+      !vsa_aligned<4>(lse, delta, counts, offsets, inverse, kv_vbs, slot_rows, tile_order))
+    return VSA_ERR_ALIGN;
   if (bh <= 0 || sq <= 0 || skv <= 0 || be <= 0 || sq % be || skv % be || topk < 1 ||
       s_out <= 0 || s_out > skv || sq > (1LL << 31) / 256 || skv > (1LL << 31) / 256)
     return VSA_ERR_SHAPE;

@@ -729,6 +729,9 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                               int32_t gate_heads, int64_t bh, int64_t sq, int64_t skv, int32_t D,
                               int32_t be, int32_t topk, float scale, int32_t dtype, void* stream) {
   if (!q || !k || !v || !selected || !kv_vbs || !out) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, out, fine_out, out_c, gate) ||
+      !vsa_aligned<4>(selected, kv_vbs, lse))
+    return VSA_ERR_ALIGN;
   if (out_c && (gate_mode & VSA_GATE_F32) && dtype != VSA_F32) {
     // fp32 gate beside T inputs: fine output in T (into fine_out, or into out
     // when no backward needs it), then the combine as a second pass
@@ -792,6 +795,9 @@ extern "C" int vsa_sparse_fwd_tiled(const void* q, const void* k, const void* v,
                                     int64_t sq, int64_t skv, int32_t D, int32_t be, int32_t topk,
                                     float scale, int32_t dtype, void* stream) {
   if (!q || !k || !v || !selected || !kv_vbs || !out || !slot_rows) return VSA_ERR_NULL;
+  if (!vsa_aligned<16>(q, k, v, out, fine_out, out_c, gate) ||
+      !vsa_aligned<4>(selected, kv_vbs, lse, slot_rows))
+    return VSA_ERR_ALIGN;
   if (gate_mode < 0 || gate_mode > 2) return VSA_ERR_SHAPE;  // no token-major / fp32 gate here
   if (out_c && gate_mode != 0 && !gate) return VSA_ERR_NULL;
   if (!out_c) {

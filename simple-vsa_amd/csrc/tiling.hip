@@ -194,6 +194,9 @@ extern "C" int vsa_tile_metadata(int32_t T, int32_t H, int32_t W, int32_t ts, in
                                  int64_t* variable_block_sizes, void* stream) {
   if (!tile_partition_indices || !reverse_indices || !non_pad_index || !variable_block_sizes)
     return VSA_ERR_NULL;
+  if (!vsa_aligned<8>(tile_partition_indices, reverse_indices, non_pad_index,
+                      variable_block_sizes))
+    return VSA_ERR_ALIGN;
   if (T <= 0 || H <= 0 || W <= 0 || ts <= 0 || hs <= 0 || ws <= 0) return VSA_ERR_SHAPE;
   const int64_t S = (int64_t)T * H * W;
   const int NT = (T + ts - 1) / ts, NH = (H + hs - 1) / hs, NW = (W + ws - 1) / ws;
@@ -212,6 +215,7 @@ extern "C" int vsa_tile_metadata(int32_t T, int32_t H, int32_t W, int32_t ts, in
 extern "C" int vsa_tile_slot_rows(int32_t T, int32_t H, int32_t W, int32_t ts, int32_t hs,
                                   int32_t ws, int32_t* slot_rows, void* stream) {
   if (!slot_rows) return VSA_ERR_NULL;
+  if (!vsa_aligned<4>(slot_rows)) return VSA_ERR_ALIGN;
   if (T <= 0 || H <= 0 || W <= 0 || ts <= 0 || hs <= 0 || ws <= 0) return VSA_ERR_SHAPE;
   const int64_t S = (int64_t)T * H * W;
   const int NT = (T + ts - 1) / ts, NH = (H + hs - 1) / hs, NW = (W + ws - 1) / ws;
@@ -232,6 +236,7 @@ extern "C" int vsa_rows_move(const void* x, int64_t x_rows, int64_t x_row_bytes,
                              const int64_t* dst_outer, int64_t n, void* stream) {
   if (!x || !out) return VSA_ERR_NULL;
   if ((src_outer && !src) || (dst_outer && !dst)) return VSA_ERR_NULL;
+  if (!vsa_aligned<8>(src, src_outer, dst, dst_outer)) return VSA_ERR_ALIGN;
   if (x_rows < 0 || out_rows < 0 || batch < 0 || n < 0 || copy_bytes <= 0 ||
       copy_bytes > x_row_bytes || copy_bytes > out_row_bytes)
     return VSA_ERR_SHAPE;
@@ -261,6 +266,7 @@ extern "C" int vsa_rows_zero_unmarked(void* out, int64_t out_rows, int64_t batch
                                       int64_t row_bytes, const int64_t* marked, int64_t n_marked,
                                       uint8_t* mark_workspace, void* stream) {
   if (!out || !mark_workspace || (n_marked > 0 && !marked)) return VSA_ERR_NULL;
+  if (!vsa_aligned<8>(marked)) return VSA_ERR_ALIGN;
   if (out_rows < 0 || batch < 0 || row_bytes <= 0 || n_marked < 0) return VSA_ERR_SHAPE;
   if (out_rows == 0 || batch == 0) return VSA_OK;
   if (out_rows > (1LL << 38) || n_marked > (1LL << 38)) return VSA_ERR_SHAPE;

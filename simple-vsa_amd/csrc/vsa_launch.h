@@ -37,6 +37,15 @@
     }                                         \
   } while (0)
 
+// Alignment the kernels' accesses need (NULL, an absent optional buffer,
+// passes): 16 bytes for rows of the element type and the fp32 score /
+// probability rows, 8 for int64 index arrays, 4 for int32 arrays and
+// lse / delta.
+template <unsigned A, typename... P>
+static inline bool vsa_aligned(P... p) {
+  return ((((uintptr_t)(const void*)p) % A == 0) && ...);
+}
+
 static inline int vsa_check_launch() {
   return hipGetLastError() == hipSuccess ? VSA_OK : VSA_ERR_LAUNCH;
 }

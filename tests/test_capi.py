@@ -3,6 +3,7 @@ every entry point ``include/vsa_capi.h`` declares, reports status text, and
 the Python layer raises the reference's ValueError texts before any launch
 (tests/test_torch_vsa.py:112-130)."""
 
+import ctypes
 import os
 import re
 
@@ -82,6 +83,31 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
                                            7, None) == -3              # no dtype 7
     assert lib.vsa_sparse_bwd_dkdv_noalloc(*([None] + noalloc[1:]), 1, 1024, 1024, 128, 256, 8,
                                            0.1, 0, None) == -1
+    # alignment (checked before any launch, nothing is dereferenced): rows of the
+    # element type 16 bytes, int32 arrays and lse / delta 4, int64 indices 8
+    buf = torch.zeros(256)
+    a16 = (buf.data_ptr() + 15) // 16 * 16
+
+    def at(off):
+        return ctypes.c_void_p(a16 + off)
+
+    assert "misaligned" in _lib.status_string(-7)
+    assert lib.vsa_pool_qkv(at(2), p, p, p, p, p, p, p, 1, 64, 64, 128, 64, 0, None) == -7
+    assert lib.vsa_pool_qkv(p, p, p, at(2), p, p, p, p, 1, 64, 64, 128, 64, 0, None) == -7
+    assert lib.vsa_sparse_fwd(p, at(8), p, p, p, p, None, None, None, None, 0, 0,
+                              1, 64, 64, 128, 64, 1, 0.1, 0, None) == -7   # k at 8 bytes
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, p, at(4), 1, 0,
+                              1, 64, 64, 128, 64, 1, 0.1, 0, None) == -7   # gate at 4 bytes
+    # an int32 route 4 bytes past a 16-byte boundary passes; the shape check fails next
+    assert lib.vsa_sparse_fwd(p, p, p, at(4), p, p, None, None, None, None, 0, 0,
+                              1, 100, 128, 128, 64, 1, 0.1, 0, None) == -2
+    assert lib.vsa_bwd_prep(p, p, None, None, 0, 0, at(2), None, None, 1, 64, 128, 64, 0,
+                            None) == -7                                    # delta at 2 bytes
+    assert lib.vsa_sparse_bwd_dkdv_noalloc(*noalloc[:10], at(16), at(24), None, None, 1, 1024,
+                                           1024, 128, 256, 8, 0.1, 0, None) == -7  # dv at 8
+    assert lib.vsa_csr_build(p, p, at(2), p, 1, 4, 4, 2, None) == -7
+    assert lib.vsa_rows_move(p, 4, 16, p, 4, 16, 16, 1, at(4), 4, None, None, 0, None, 4,
+                             None) == -7                                   # int64 at 4 bytes
     # tiling entry points validate before launching
     assert lib.vsa_tile_metadata(0, 4, 4, 2, 2, 2, p, p, p, p, None) == -2
     assert lib.vsa_tile_metadata(4, 4, 4, 2, 2, 2, None, p, p, p, None) == -1
