@@ -981,7 +981,9 @@ __device__ __forceinline__ void dq_pp_tile(
   if (grp1) phase_barrier();
   if (nv0 > 0) {
     phase_barrier();
+    mfma_priority_up();
     mma_x(0, 0, NoDq{});
+    mfma_priority_down();
     dma_wait();  // this wave's copies of chunk 1
     phase_barrier();
     int nv2 = issue(2);
@@ -997,7 +999,9 @@ __device__ __forceinline__ void dq_pp_tile(
       if (fin > 0) valu(fin);
       prefetch((j - 1) % C::NS);
       phase_barrier();
+      mfma_priority_up();
       mma_x(j % C::NS, (j - 1) % C::NS, WithDq{});
+      mfma_priority_down();
       dma_wait();  // this wave's copies of chunk j+1
       phase_barrier();
       nv2 = issue((j + 2) % C::NS);

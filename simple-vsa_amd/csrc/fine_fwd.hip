@@ -595,8 +595,10 @@ __device__ __forceinline__ void fwd_pp_tile(
   if (nv0 > 0) {
     // chunk 0: no chunk -1, so its MFMA phase is S_0 alone
     phase_barrier();
+    mfma_priority_up();
     mma_s(0);
     prep_all(nv0);
+    mfma_priority_down();
     dma_wait();  // this wave's copies of chunk 1
     phase_barrier();
     int nv2 = issue(2);
@@ -617,7 +619,9 @@ __device__ __forceinline__ void fwd_pp_tile(
       if (grp1) dma_wait();  // this wave's copies of chunk j+1
       prefetch(j % C::NS);
       phase_barrier();
+      mfma_priority_up();
       mma_so(j % C::NS, (j - 1) % C::NS, nv0);
+      mfma_priority_down();
       if (!grp1) dma_wait();  // this wave's copies of chunk j+1
       phase_barrier();
       // the stage of chunk j+2 last held chunk j-2, read for the last time in

@@ -366,6 +366,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Wait for this wave's outstanding vector-memory loads (vmcnt = 0).
 __device__ __forceinline__ void dma_wait() { wait_vmcnt<0>(); }
 
+// Issue priority of this wave over the other wave of its SIMD (s_setprio), for
+// the ping-pong kernels: raised for an MFMA phase, so that its MFMAs and LDS
+// operand reads win issue arbitration over the other wave's VALU phase, and
+// lowered after it.  The scheduler keeps the phase's work between the two.
+__device__ __forceinline__ void mfma_priority_up() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(1);
+  __builtin_amdgcn_sched_barrier(0);
+}
+__device__ __forceinline__ void mfma_priority_down() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(0);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // exp2 on the transcendental unit without the libm range fix-ups
 // (results below 2^-126 flush to zero, which softmax weights tolerate).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
