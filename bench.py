@@ -391,7 +391,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)   # BASELINE: >= 10 warm-up iterations
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--kernels-only", action="store_true", help="skip the CPU baseline and summary")
     ap.add_argument("--copy-probe", action="store_true",
@@ -522,6 +522,19 @@ def main():
     for n, (t, f) in kt.items():
         if f:
             kernels[n]["tflops_algorithmic"] = round(f / (t * 1e-3) / 1e12, 1)
+    # the bandwidth kernels against the HBM peak, on the bytes each must move
+    # once: pooling reads q, k, v and writes the block means; bwd_prep (delta and
+    # the combine backward) reads the fine output, dO and the gate and writes
+    # d_gate and delta (the block-sized out_c / d_out_c are counted too)
+    tok = qd.numel() * qd.element_size()
+    pooled = B * H * nb * D * qd.element_size()
+    gbytes = gd.numel() * gd.element_size() if gd is not None else 0
+    bw_bytes = {"pool_qkv": 3 * tok + 3 * pooled,
+                "bwd_prep": 2 * tok + 2 * gbytes + B * H * S * 4 + 2 * pooled}
+    for n, nbytes in bw_bytes.items():
+        gbs = nbytes / (kt[n][0] * 1e-3) / 1e9
+        kernels[n]["gbs_algorithmic"] = round(gbs, 1)
+        kernels[n]["frac_hbm_peak"] = round(gbs / HBM_PEAK_GBS, 3)
     dom = max((n for n in kt if kt[n][1]), key=lambda n: kt[n][0])
     dom_t, dom_f = kt[dom]
     achieved = dom_f / (dom_t * 1e-3) / 1e12
