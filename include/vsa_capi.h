@@ -95,7 +95,9 @@ int vsa_pool_qkv(const void* q, const void* k, const void* v,
  *   out_c[bh, i, :]  = T(sum_j probs[i, j] * v_c[j, :])
  *   selected[bh, i, :] = the `topk` key blocks with the largest scores; ties go
  *   to the smaller block id; written in ascending block-id order (int32).
- * `selected` may be NULL (no routing).  Kb <= 8192.
+ * `selected` may be NULL (no routing).  Kb <= 16000 for bf16 / fp16 at head
+ * dims 64 and 128 (MFMA kernels streaming key tiles; the Top-K keeps one row
+ * of Kb keys in LDS), Kb <= 4096 otherwise (generic kernels, two rows in LDS).
  */
 int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
                    float* scores, float* probs, void* out_c, int32_t* selected,
@@ -105,7 +107,7 @@ int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
 /*
  * Stand-alone Top-K over fp32 scores [rows, kv_blocks] -> int32 [rows, topk]
  * with the same tie rule and output order as vsa_coarse_fwd.
- * Replaces scores.topk(topk, dim=-1) (triton_impl.py:1710).
+ * Replaces scores.topk(topk, dim=-1) (triton_impl.py:1710).  kv_blocks <= 16000.
  */
 int vsa_topk(const float* scores, int32_t* selected, int64_t rows,
              int32_t kv_blocks, int32_t topk, void* stream);
@@ -115,7 +117,8 @@ int vsa_topk(const float* scores, int32_t* selected, int64_t rows,
  * Replaces _invert_indices (triton_impl.py:544-595): counts [BH, Kb],
  * offsets [BH, Kb] (exclusive prefix of counts), inverse [BH, Qb*topk].
  * Unlike the reference's atomic cursor, every segment is written in ascending
- * query-block order, so the result is deterministic.
+ * query-block order, so the result is deterministic.  q_blocks, kv_blocks
+ * <= 16000 (one row of counts, and one of query blocks, in LDS).
  */
 int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
                   int32_t* inverse, int64_t bh, int32_t q_blocks, int32_t kv_blocks,
@@ -167,7 +170,7 @@ int vsa_bwd_prep(const void* fine_out, const void* dout, const void* out_c, cons
  *   dP = T(d_out_c v_c^T); d_v_c = T(P^T d_out_c);
  *   dS = T(scale * T(P * (dP - rowsum(P * dP))));
  *   d_q_c = T(dS k_c); d_k_c = T(dS^T q_c).
- * `ds` is fp32 workspace [BH, Qb, Kb].
+ * `ds` is fp32 workspace [BH, Qb, Kb].  Kb limits as for vsa_coarse_fwd.
  */
 int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c, const float* probs,
                    const void* d_out_c, float* ds, void* d_q_c, void* d_k_c, void* d_v_c,

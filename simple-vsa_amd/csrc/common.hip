@@ -154,7 +154,14 @@ __global__ __launch_bounds__(256) void tile_pool_kernel(
   }
 }
 
-constexpr int kMaxCoarseBlocks = 4096;  // generic kernels keep [2 Kb + D] fp32 rows in LDS
+// Key blocks per sequence: the generic coarse kernels keep [2 Kb + D] fp32 rows
+// in LDS; the MFMA coarse kernels stream key tiles, and the Top-K keeps one
+// row of Kb keys in LDS (64 KiB with its histogram).
+constexpr int kMaxCoarseBlocks = 4096;
+constexpr int kMaxRouteBlocks = 16000;
+static int max_coarse_blocks(int D, int dtype) {
+  return coarse_mfma_supported(D, dtype) ? kMaxRouteBlocks : kMaxCoarseBlocks;
+}
 
 // Generic coarse forward (fp32, or head dims the MFMA kernels do not take):
 // one workgroup per (bh, query block); scores in T, softmax in T, out_c in T
@@ -242,23 +249,19 @@ __global__ __launch_bounds__(256) void csr_scatter_kernel(
     const int32_t* __restrict__ selected, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ inverse, int qb, int kb, int topk) {
   extern __shared__ int ismem[];
-  int* cnt = ismem;        // kb
-  int* cur = cnt + kb;     // kb
+  int* cur = ismem;        // kb: counts, then (after the scan) the write cursors
   int* tmp = cur + kb;     // 256
   const int64_t b = blockIdx.x;
   const int edges = qb * topk;
   const int32_t* sel = selected + b * edges;
-  for (int j = threadIdx.x; j < kb; j += 256) cnt[j] = 0;
+  for (int j = threadIdx.x; j < kb; j += 256) cur[j] = 0;
   __syncthreads();
   for (int e = threadIdx.x; e < edges; e += 256) {
     const int kv = sel[e];
-    if (kv >= 0 && kv < kb) atomicAdd(&cnt[kv], 1);
+    if (kv >= 0 && kv < kb) atomicAdd(&cur[kv], 1);
   }
   __syncthreads();
-  for (int j = threadIdx.x; j < kb; j += 256) {
-    counts[b * kb + j] = cnt[j];
-    cur[j] = cnt[j];
-  }
+  for (int j = threadIdx.x; j < kb; j += 256) counts[b * kb + j] = cur[j];
   __syncthreads();
   block_exclusive_scan(cur, kb, tmp);
   for (int j = threadIdx.x; j < kb; j += 256) offsets[b * kb + j] = cur[j];
@@ -678,7 +681,7 @@ extern "C" int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
   if (!q_c || !k_c || !v_c || !scores || !probs || !out_c) return VSA_ERR_NULL;
   if (!vsa_aligned<16>(q_c, k_c, v_c, scores, probs, out_c) || !vsa_aligned<4>(selected))
     return VSA_ERR_ALIGN;
-  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
+  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > max_coarse_blocks(D, dtype) || D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   if (selected && (topk < 1 || topk > kb)) return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
@@ -703,11 +706,11 @@ extern "C" int vsa_topk(const float* scores, int32_t* selected, int64_t rows, in
                         int32_t topk, void* stream) {
   if (!scores || !selected) return VSA_ERR_NULL;
   if (!vsa_aligned<16>(scores) || !vsa_aligned<4>(selected)) return VSA_ERR_ALIGN;
-  if (rows <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || topk < 1 || topk > kb) return VSA_ERR_SHAPE;
+  if (rows <= 0 || kb <= 0 || kb > kMaxRouteBlocks || topk < 1 || topk > kb) return VSA_ERR_SHAPE;
   return topk_radix(scores, selected, rows, kb, topk, (hipStream_t)stream);
 }
 
-constexpr int kMaxCsrBlocks = 8064;  // 2*Kb + 256 ints of LDS stay under 64 KiB
+constexpr int kMaxCsrBlocks = 16000;  // Kb (or Qb) + 256 ints of LDS stay under 64 KiB
 
 extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
                              int32_t* inverse, int64_t bh, int32_t qb, int32_t kb, int32_t topk,
@@ -719,7 +722,7 @@ extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* 
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(csr_scatter_kernel, dim3((unsigned)bh), dim3(256),
-                     (size_t)(2 * kb + 256) * sizeof(int), s, selected, counts, offsets, inverse,
+                     (size_t)(kb + 256) * sizeof(int), s, selected, counts, offsets, inverse,
                      qb, kb, topk);
   int rc = vsa_check_launch();
   if (rc) return rc;
@@ -810,7 +813,7 @@ extern "C" int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c,
     return VSA_ERR_NULL;
   if (!vsa_aligned<16>(q_c, k_c, v_c, probs, d_out_c, ds, d_q_c, d_k_c, d_v_c))
     return VSA_ERR_ALIGN;
-  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > kMaxCoarseBlocks || D <= 0 || D > 1024)
+  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > max_coarse_blocks(D, dtype) || D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   if (coarse_mfma_supported(D, dtype))

@@ -44,6 +44,10 @@ SUPPORTED_BLOCKS = (64, 128, 256)
 SUPPORTED_HEAD_DIMS = (64, 128, 256)
 KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 MFMA_DTYPES = (torch.bfloat16, torch.float16)
+# blocks per sequence: the Top-K and the backward's CSR keep one row of blocks
+# in LDS; the generic coarse kernels (fp32, head dims above 128) keep two
+MAX_ROUTE_BLOCKS = 16000
+MAX_COARSE_BLOCKS = 4096
 
 
 # ---------------------------------------------------------------------------
@@ -84,9 +88,10 @@ def validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, t
         raise ValueError(f"topk must be in [1, {kb}]")
 
 
-def _check_device_path(q, k, v, block_elements) -> None:
+def _check_device_path(q, k, v, block_elements, coarse=True) -> None:
     """Constraints of the gfx950 kernels (the reference's GPU checks,
-    triton_impl.py:371-384, narrowed to the shapes that have MI355X kernels)."""
+    triton_impl.py:371-384, narrowed to the shapes that have MI355X kernels).
+    ``coarse``: the op runs the coarse branch (not the explicit route)."""
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise ValueError("the MI355X implementation requires GPU tensors")
     if not (q.device == k.device == v.device):
@@ -97,6 +102,19 @@ def _check_device_path(q, k, v, block_elements) -> None:
         raise ValueError("the MI355X kernels support float16, bfloat16 and float32")
     _kernel_block(block_elements)
     _kernel_dim(q.shape[-1])
+    if q.ndim == 4 and k.ndim == 4 and block_elements > 0:
+        nblocks = max(-(-q.shape[-2] // block_elements), -(-k.shape[-2] // block_elements))
+        _check_block_count(nblocks, q, coarse)
+
+
+def _check_block_count(nblocks: int, q: Tensor, coarse: bool = True) -> None:
+    """At most MAX_ROUTE_BLOCKS blocks per sequence, MAX_COARSE_BLOCKS where the
+    coarse branch runs on its generic kernels (fp32, or head dims above 128)."""
+    generic = coarse and not (q.dtype in MFMA_DTYPES and _kernel_dim(q.shape[-1]) <= 128)
+    limit = MAX_COARSE_BLOCKS if generic else MAX_ROUTE_BLOCKS
+    if nblocks > limit:
+        raise ValueError(f"the MI355X kernels support at most {limit} blocks per sequence "
+                         f"here ({nblocks} given)")
 
 
 def _kernel_block(be: int) -> int:
@@ -447,7 +465,7 @@ def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
     be = as_block_elements(block_size)
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k, and v must have shape [batch, heads, seq_len, dim]")
-    _check_device_path(q, k, v, be)
+    _check_device_path(q, k, v, be, coarse=False)
     _validate_route(q, k, selected, variable_block_sizes, be)
     if q.shape[0] * q.shape[1] == 0:
         return _empty_batch(q, k, v)

@@ -194,7 +194,7 @@ def mi355x_sparse_attention(q: Tensor, k: Tensor, v: Tensor, selected: Tensor,
     be = M.as_block_elements(block_size)
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k, and v must have shape [batch, heads, seq_len, dim]")
-    M._check_device_path(q, k, v, be)
+    M._check_device_path(q, k, v, be, coarse=False)
     M._validate_route(q, k, selected, variable_block_sizes, be)
     if q.shape[0] * q.shape[1] == 0 or M._padded(q, k, be) is not None:
         return M.mi355x_sparse_attention(q, k, v, selected, variable_block_sizes,

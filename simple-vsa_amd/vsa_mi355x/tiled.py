@@ -235,6 +235,7 @@ def mi355x_vsa_tiled(q: Tensor, k: Tensor, v: Tensor, dit_seq_shape: Tuple[int, 
     be = math.prod(ts)
     nb = math.ceil(shape[0] / ts[0]) * math.ceil(shape[1] / ts[1]) * math.ceil(shape[2] / ts[2])
     M._check_device_path(q, k, v, be)
+    M._check_block_count(nb, q)
     if q.shape[0] * (q.shape[2] if token_major else q.shape[1]) == 0:
         return M._empty_batch(q, k, v, compress_attn_weight)
     gate = compress_attn_weight

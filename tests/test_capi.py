@@ -108,6 +108,15 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.vsa_csr_build(p, p, at(2), p, 1, 4, 4, 2, None) == -7
     assert lib.vsa_rows_move(p, 4, 16, p, 4, 16, 16, 1, at(4), 4, None, None, 0, None, 4,
                              None) == -7                                   # int64 at 4 bytes
+    # blocks per sequence: 16000 for the route, the CSR and the MFMA coarse
+    # kernels (bf16 / fp16 at head dims 64, 128), 4096 for the generic ones
+    assert lib.vsa_topk(p, p, 1, 16001, 2, None) == -2
+    assert lib.vsa_csr_build(p, p, p, p, 1, 4, 16001, 2, None) == -2
+    assert lib.vsa_csr_build(p, p, p, p, 1, 16001, 4, 2, None) == -2
+    assert lib.vsa_coarse_fwd(p, p, p, p, p, p, None, 1, 4, 16001, 128, 2, 0.1, 0, None) == -2
+    assert lib.vsa_coarse_fwd(p, p, p, p, p, p, None, 1, 4, 4097, 128, 2, 0.1, 2, None) == -2
+    assert lib.vsa_coarse_fwd(p, p, p, p, p, p, None, 1, 4, 4097, 256, 2, 0.1, 0, None) == -2
+    assert lib.vsa_coarse_bwd(*([p] * 9), 1, 4, 4097, 96, 0.1, 1, None) == -2
     # tiling entry points validate before launching
     assert lib.vsa_tile_metadata(0, 4, 4, 2, 2, 2, p, p, p, p, None) == -2
     assert lib.vsa_tile_metadata(4, 4, 4, 2, 2, 2, None, p, p, p, None) == -1
@@ -201,3 +210,14 @@ def test_kernel_shape_mapping_and_limits():
         M._kernel_dim(257)
     rows = M._block_rows(12, 3, 64, torch.device("cpu"))
     assert rows.tolist() == [0, 1, 2, 64, 65, 66, 128, 129, 130, 192, 193, 194]
+    # blocks per sequence (the route / CSR rows in LDS; the generic coarse kernels)
+    bf, f32 = torch.zeros(1, 1, 1, 96, dtype=torch.bfloat16), torch.zeros(1, 1, 1, 64)
+    M._check_block_count(16000, bf)
+    with pytest.raises(ValueError, match="at most 16000 blocks"):
+        M._check_block_count(16001, bf)
+    M._check_block_count(4096, f32)
+    with pytest.raises(ValueError, match="at most 4096 blocks"):
+        M._check_block_count(4097, f32)
+    with pytest.raises(ValueError, match="at most 4096 blocks"):   # head dim 256: generic coarse
+        M._check_block_count(4097, torch.zeros(1, 1, 1, 200, dtype=torch.float16))
+    M._check_block_count(16000, f32, coarse=False)                 # explicit route: no coarse
