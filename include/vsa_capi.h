@@ -26,6 +26,8 @@
  *  - launches are asynchronous on `stream`; no host synchronisation;
  *  - return 0 on success, a negative VSA_ERR_* code otherwise (no exceptions
  *    cross the ABI); vsa_status_string() turns a code into text;
+ *  - BH <= 65535 (the per-(batch, head) passes put it in the grid's y
+ *    dimension);
  *  - route ids outside [0, Kb) contribute nothing; block sizes are clamped to
  *    [0, block_elements] for token masking.
  */

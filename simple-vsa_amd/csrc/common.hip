@@ -159,6 +159,8 @@ __global__ __launch_bounds__(256) void tile_pool_kernel(
 // row of Kb keys in LDS (64 KiB with its histogram).
 constexpr int kMaxCoarseBlocks = 4096;
 constexpr int kMaxRouteBlocks = 16000;
+// batch * heads: the per-(batch, head) passes put it in the grid's y dimension
+constexpr int64_t kMaxGridY = 65535;
 static int max_coarse_blocks(int D, int dtype) {
   return coarse_mfma_supported(D, dtype) ? kMaxRouteBlocks : kMaxCoarseBlocks;
 }
@@ -681,7 +683,8 @@ extern "C" int vsa_coarse_fwd(const void* q_c, const void* k_c, const void* v_c,
   if (!q_c || !k_c || !v_c || !scores || !probs || !out_c) return VSA_ERR_NULL;
   if (!vsa_aligned<16>(q_c, k_c, v_c, scores, probs, out_c) || !vsa_aligned<4>(selected))
     return VSA_ERR_ALIGN;
-  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > max_coarse_blocks(D, dtype) || D <= 0 || D > 1024)
+  if (bh <= 0 || bh > kMaxGridY || qb <= 0 || kb <= 0 || kb > max_coarse_blocks(D, dtype) ||
+      D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   if (selected && (topk < 1 || topk > kb)) return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
@@ -717,7 +720,8 @@ extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* 
                              void* stream) {
   if (!selected || !counts || !offsets || !inverse) return VSA_ERR_NULL;
   if (!vsa_aligned<4>(selected, counts, offsets, inverse)) return VSA_ERR_ALIGN;
-  if (bh <= 0 || qb <= 0 || kb <= 0 || topk <= 0 || kb > kMaxCsrBlocks || qb > kMaxCsrBlocks ||
+  if (bh <= 0 || bh > kMaxGridY || qb <= 0 || kb <= 0 || topk <= 0 || kb > kMaxCsrBlocks ||
+      qb > kMaxCsrBlocks ||
       (int64_t)qb * topk > (1 << 30))
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
@@ -745,7 +749,8 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
   if (out_c && !d_out_c) return VSA_ERR_NULL;
   if (out_c && gate_mode != 0 && (!gate || !d_gate)) return VSA_ERR_NULL;
   if (!out_c) gate_mode = 0;
-  if (bh <= 0 || be <= 0 || sq <= 0 || sq % be || !vec_dim_ok(D, dtype)) return VSA_ERR_SHAPE;
+  if (bh <= 0 || bh > kMaxGridY || be <= 0 || sq <= 0 || sq % be || !vec_dim_ok(D, dtype))
+    return VSA_ERR_SHAPE;
   const int qb = (int)(sq / be);
   hipStream_t s = (hipStream_t)stream;
   VSA_DISPATCH_ALL(dtype, T, {
@@ -776,7 +781,7 @@ extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const 
   if (out_c && !d_out_c) return VSA_ERR_NULL;
   if (out_c && gate_mode != 0 && (!gate || !d_gate)) return VSA_ERR_NULL;
   if (!out_c) gate_mode = 0;
-  if (bh <= 0 || be <= 0 || sq <= 0 || sq % be || s_out <= 0 || s_out > sq ||
+  if (bh <= 0 || bh > kMaxGridY || be <= 0 || sq <= 0 || sq % be || s_out <= 0 || s_out > sq ||
       !vec_dim_ok(D, dtype))
     return VSA_ERR_SHAPE;
   const int qb = (int)(sq / be);
@@ -794,7 +799,8 @@ namespace vsa {
 int combine_f32gate(const void* fine, const void* out_c, const void* gate, int gate_mode,
                     int gate_heads, void* out, int64_t bh, int64_t sq, int D, int be, int dtype,
                     hipStream_t s) {
-  if (bh <= 0 || be <= 0 || sq <= 0 || sq % be || !vec_dim_ok(D, dtype)) return VSA_ERR_SHAPE;
+  if (bh <= 0 || bh > kMaxGridY || be <= 0 || sq <= 0 || sq % be || !vec_dim_ok(D, dtype))
+    return VSA_ERR_SHAPE;
   const int qb = (int)(sq / be);
   VSA_DISPATCH_ALL(dtype, T, {
     hipLaunchKernelGGL((combine_f32gate_kernel<T>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
@@ -813,7 +819,8 @@ extern "C" int vsa_coarse_bwd(const void* q_c, const void* k_c, const void* v_c,
     return VSA_ERR_NULL;
   if (!vsa_aligned<16>(q_c, k_c, v_c, probs, d_out_c, ds, d_q_c, d_k_c, d_v_c))
     return VSA_ERR_ALIGN;
-  if (bh <= 0 || qb <= 0 || kb <= 0 || kb > max_coarse_blocks(D, dtype) || D <= 0 || D > 1024)
+  if (bh <= 0 || bh > kMaxGridY || qb <= 0 || kb <= 0 || kb > max_coarse_blocks(D, dtype) ||
+      D <= 0 || D > 1024)
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   if (coarse_mfma_supported(D, dtype))

@@ -48,6 +48,8 @@ MFMA_DTYPES = (torch.bfloat16, torch.float16)
 # in LDS; the generic coarse kernels (fp32, head dims above 128) keep two
 MAX_ROUTE_BLOCKS = 16000
 MAX_COARSE_BLOCKS = 4096
+# the per-(batch, head) passes put batch * heads in the grid's y dimension
+MAX_BATCH_HEADS = 65535
 
 
 # ---------------------------------------------------------------------------
@@ -105,6 +107,8 @@ def _check_device_path(q, k, v, block_elements, coarse=True) -> None:
     if q.ndim == 4 and k.ndim == 4 and block_elements > 0:
         nblocks = max(-(-q.shape[-2] // block_elements), -(-k.shape[-2] // block_elements))
         _check_block_count(nblocks, q, coarse)
+    if q.ndim == 4 and q.shape[0] * q.shape[1] > MAX_BATCH_HEADS:
+        raise ValueError(f"the MI355X kernels support batch * heads <= {MAX_BATCH_HEADS}")
 
 
 def _check_block_count(nblocks: int, q: Tensor, coarse: bool = True) -> None:

@@ -234,7 +234,8 @@ def mi355x_vsa_tiled(q: Tensor, k: Tensor, v: Tensor, dit_seq_shape: Tuple[int, 
                              "that broadcasts to it (e.g. [batch, heads, seq_len, 1])")
     be = math.prod(ts)
     nb = math.ceil(shape[0] / ts[0]) * math.ceil(shape[1] / ts[1]) * math.ceil(shape[2] / ts[2])
-    M._check_device_path(q, k, v, be)
+    # the checks read [B, H, S, D] shapes: token-major tensors as head-major views
+    M._check_device_path(*(x.transpose(1, 2) if token_major else x for x in (q, k, v)), be)
     M._check_block_count(nb, q)
     if q.shape[0] * (q.shape[2] if token_major else q.shape[1]) == 0:
         return M._empty_batch(q, k, v, compress_attn_weight)

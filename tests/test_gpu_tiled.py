@@ -69,6 +69,9 @@ CASES = [
     ((6, 16, 24), (4, 8, 8), 22, 128, torch.float16, "token", 3),   # block 256, ping-pong kernels
     ((3, 9, 10), (2, 8, 8), 3, 128, torch.bfloat16, None, 2),       # block 128, no gate
     ((6, 16, 24), (4, 8, 8), 2, 64, torch.bfloat16, "full", 5),     # block 256, 4-wave kernels
+    # 81 920 tokens: batch * seq_len of a token-major [B, S, H, D] tensor exceeds
+    # the 65 535 batch * heads bound, which must not be mistaken for it
+    ((4, 128, 160), (4, 8, 8), 2, 64, torch.bfloat16, None, 4),
 ]
 
 
@@ -140,7 +143,7 @@ def test_fused_tiled_op_at_c3_size_equals_the_composition():
         assert torch.equal(a, b), (name, (a.float() - b.float()).abs().max().item())
 
 
-@pytest.mark.parametrize("case", [0, 1])
+@pytest.mark.parametrize("case", [0, 1, 4])
 def test_token_major_tiled_op_equals_head_major_and_composition(case):
     """q, k, v, gate, dout as [B, S, H, D] (the projection's layout, tile()'s
     [batch, seq, ...]): the same values as the head-major op, transposed, and
