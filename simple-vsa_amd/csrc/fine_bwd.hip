@@ -539,9 +539,6 @@ __device__ __forceinline__ void dkdv_tile(
       for (int u = 0; u < NA; ++u) {
         issue(u + L);
 #pragma unroll
-        for (int p = 0; p < C::PER; ++p)
-          if ((p * NA) / C::PER == u) copy_piece(cp, SP, p);
-#pragma unroll
         for (int t = 0; t < KTL; ++t) {
           if (u & 1)
             pn[t] = E::mfma32(op[u], vf[t][u >> 1], pn[t]);
@@ -568,6 +565,13 @@ __device__ __forceinline__ void dkdv_tile(
           else
             dvacc[mt][t] = E::mfma32(op[NA + vv], bp[t][j], dvacc[mt][t]);
         }
+        // the copy of item it+NS-1, spread over the second half of the dV / dK
+        // MFMAs, which carries no P / dS arithmetic: a copy stalls its wave on
+        // the address unit, and there the stall overlaps MFMAs only (2 % less
+        // step time than spreading them over the S / dP MFMAs, bit-identical)
+#pragma unroll
+        for (int p = 0; p < C::PER; ++p)
+          if (NC / 2 + (p * (NC / 2)) / C::PER == vv) copy_piece(cp, SP, p);
         if (vv < NC / 2) b_slot(NA + vv);
         if (vv == NC / 2 - 1) {
 #pragma unroll
