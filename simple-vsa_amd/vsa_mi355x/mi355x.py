@@ -36,6 +36,7 @@ from typing import Optional, Tuple, Union
 
 import torch
 from torch import Tensor
+from torch.autograd.function import once_differentiable
 
 from . import _lib
 from .tiling import _move, _zero_unmarked
@@ -147,7 +148,9 @@ def _block_rows(s: int, be: int, kbe: int, device: torch.device) -> Tensor:
 
 
 class _Pad(torch.autograd.Function):
-    """[B, H, S, d] -> [B, H, (S/be)*kbe, kd], zero rows and channels added."""
+    """[B, H, S, d] -> [B, H, (S/be)*kbe, kd], zero rows and channels added.
+    _Pad and _Unpad are each other's adjoint, so each one's backward applies the
+    other and both differentiate to any order."""
 
     @staticmethod
     def forward(ctx, x, rows, out_rows, kd):
@@ -165,7 +168,7 @@ class _Pad(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         (rows,) = ctx.saved_tensors
-        return _unpad(g, rows, ctx.shape), None, None, None
+        return _Unpad.apply(g, rows, ctx.shape), None, None, None
 
 
 def _unpad(x: Tensor, rows: Tensor, shape) -> Tensor:
@@ -438,6 +441,7 @@ class _SparseAttention(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dout):
         q, k, v, out, lse, selected, vbs = ctx.saved_tensors
         dout = _aligned16(dout.contiguous())
@@ -522,6 +526,7 @@ class _VSA(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dout):
         q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, fine, lse = ctx.saved_tensors
         dout = _aligned16(dout.contiguous())

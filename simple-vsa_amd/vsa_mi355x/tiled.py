@@ -32,6 +32,7 @@ from typing import Optional, Tuple
 
 import torch
 from torch import Tensor
+from torch.autograd.function import once_differentiable
 
 from . import _lib
 from . import mi355x as M
@@ -110,6 +111,7 @@ class _VSATiled(torch.autograd.Function):
         return out
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dout):
         gate, rows, vbs, qvbs, qt, kt, vt, qc, kc, vc, probs, outc, sel, fine, lse = \
             ctx.saved_tensors

@@ -122,31 +122,34 @@ def _check(x: Tensor) -> Tensor:
 
 
 class _Tile(torch.autograd.Function):
+    """``out[:, dst] = x[:, src]`` along dim 1 into ``out_rows`` rows, every row
+    outside ``dst`` zero.  With unique indices its adjoint is the same move with
+    ``src`` and ``dst`` swapped into ``x``'s row count, so the backward applies
+    _Tile again and the move differentiates to any order."""
+
     @staticmethod
-    def forward(ctx, x, tpi, npi, num_blocks, max_block_size):
+    def forward(ctx, x, src, dst, out_rows):
         x = _check(x)
-        tpi, npi = _index(tpi, x.device), _index(npi, x.device)
-        if tpi.numel() != npi.numel():
+        src, dst = _index(src, x.device), _index(dst, x.device)
+        if src.numel() != dst.numel():
             raise ValueError("tile_partition_indices and non_pad_index must have the same length")
-        out = torch.empty((x.shape[0], num_blocks * max_block_size, *x.shape[2:]),
-                          dtype=x.dtype, device=x.device)
-        _zero_unmarked(out, npi)
-        _move(x, out, tpi, None, npi, None, tpi.numel())
-        ctx.save_for_backward(tpi, npi)
+        out = torch.empty((x.shape[0], out_rows, *x.shape[2:]), dtype=x.dtype, device=x.device)
+        _zero_unmarked(out, dst)
+        _move(x, out, src, None, dst, None, src.numel())
+        ctx.save_for_backward(src, dst)
         ctx.x_rows = x.shape[1]
         return out
 
     @staticmethod
     def backward(ctx, g):
-        tpi, npi = ctx.saved_tensors
-        g = g.contiguous()
-        dx = torch.empty((g.shape[0], ctx.x_rows, *g.shape[2:]), dtype=g.dtype, device=g.device)
-        _zero_unmarked(dx, tpi)
-        _move(g, dx, npi, None, tpi, None, tpi.numel())
-        return dx, None, None, None, None
+        src, dst = ctx.saved_tensors
+        return _Tile.apply(g, dst, src, ctx.x_rows), None, None, None
 
 
 class _Untile(torch.autograd.Function):
+    """``out[:, i] = x[:, npi[rev[i]]]`` for i < len(rev); its adjoint is
+    _Retile, and the two are each other's backward."""
+
     @staticmethod
     def forward(ctx, x, npi, rev):
         x = _check(x)
@@ -160,11 +163,26 @@ class _Untile(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         npi, rev = ctx.saved_tensors
-        g = g.contiguous()
-        dx = torch.empty((g.shape[0], ctx.x_rows, *g.shape[2:]), dtype=g.dtype, device=g.device)
-        _zero_unmarked(dx, npi)
-        _move(g, dx, None, None, npi, rev, rev.numel())
-        return dx, None, None
+        return _Retile.apply(g, npi, rev, ctx.x_rows), None, None
+
+
+class _Retile(torch.autograd.Function):
+    """``out[:, npi[rev[i]]] = x[:, i]`` into ``out_rows`` rows, every row
+    outside ``npi`` zero: the adjoint of _Untile."""
+
+    @staticmethod
+    def forward(ctx, x, npi, rev, out_rows):
+        x = _check(x)
+        out = torch.empty((x.shape[0], out_rows, *x.shape[2:]), dtype=x.dtype, device=x.device)
+        _zero_unmarked(out, npi)
+        _move(x, out, None, None, npi, rev, rev.numel())
+        ctx.save_for_backward(npi, rev)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        npi, rev = ctx.saved_tensors
+        return _Untile.apply(g, npi, rev), None, None, None
 
 
 def tile(x: Tensor, tile_partition_indices: Tensor, non_pad_index: Tensor, num_blocks: int,
@@ -172,8 +190,8 @@ def tile(x: Tensor, tile_partition_indices: Tensor, non_pad_index: Tensor, num_b
     """Raster-order tokens -> zero-padded tile-contiguous layout along dim 1, as
     the reference's tile (fastvideo_tiling.py:130-140): ``out[:, non_pad_index] =
     x[:, tile_partition_indices]``, every other row zero."""
-    return _Tile.apply(x, tile_partition_indices, non_pad_index, int(num_blocks),
-                       int(max_block_size))
+    return _Tile.apply(x, tile_partition_indices, non_pad_index,
+                       int(num_blocks) * int(max_block_size))
 
 
 def untile(x: Tensor, non_pad_index: Tensor, reverse_tile_partition_indices: Tensor) -> Tensor:
