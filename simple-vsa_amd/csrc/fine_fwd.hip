@@ -228,8 +228,8 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 #pragma unroll
     for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], sacc[smt][i]);
-    float smax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      for (int i = 0; i < 16; ++i) m4[i & 3] = vmax(m4[i & 3], sacc[smt][i]);
+    float smax = vmax(vmax(m4[0], m4[1]), vmax(m4[2], m4[3]));
     smax = pair_max32(smax) * c2;
     // Only the lanes whose own chunk max passed the slack move their max (the
     // branch is wave-uniform, the update is not): a row's values then never
@@ -452,14 +452,14 @@ __device__ __forceinline__ void fwd_pp_tile(
 #pragma unroll
       for (int i = 0; i < 4; ++i) m4[i] = tv[i];
 #pragma unroll
-      for (int i = 4; i < 16; ++i) m4[i & 3] = fmaxf(m4[i & 3], tv[i]);
+      for (int i = 4; i < 16; ++i) m4[i & 3] = vmax(m4[i & 3], tv[i]);
     }
     if (st == 2) {
 #pragma unroll
-      for (int i = 16; i < 32; ++i) m4[i & 3] = fmaxf(m4[i & 3], tv[i]);
+      for (int i = 16; i < 32; ++i) m4[i & 3] = vmax(m4[i & 3], tv[i]);
     }
     if (st == 3) {
-      float smax = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      float smax = vmax(vmax(m4[0], m4[1]), vmax(m4[2], m4[3]));
       smax = pair_max32(smax) * c2;
       // per-lane update under a wave-uniform branch, as in sparse_fwd_kernel
       const bool grow = smax > m + kRescaleSlack;

@@ -385,13 +385,23 @@ __device__ __forceinline__ void mfma_priority_down() {
 // (results below 2^-126 flush to zero, which softmax weights tolerate).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Maximum of two floats for the softmax row max: IEEE 754-2019 maximum (a NaN
+// operand gives NaN, -0 < +0), which gfx950 runs as v_maximum3_f32, three
+// operands per instruction.  fmaxf must quiet a signalling NaN, so the compiler
+// puts a v_max_f32 x, x in front of each operand it cannot prove canonical
+// (every MFMA result): 15 instructions for a 16-value max against 9 here.  On
+// non-NaN values both return the larger operand, so the softmax is unchanged.
+__device__ __forceinline__ float vmax(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+
 // Max / sum of the lane pair (i, i ^ 32), in both lanes, with v_permlane32_swap
 // (no LDS round trip, unlike a generic shuffle).  Both are symmetric, so the
 // two swapped halves combine without a select.
 __device__ __forceinline__ float pair_max32(float x) {
   const auto r =
       __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair_sum32(float x) {
   const auto r =
