@@ -1235,15 +1235,17 @@ extern "C" int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, co
     return sparse_dq_f32(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, q_vbs, bh, sq,
                          skv, D, be, topk, scale, s);
 #ifndef VSA_DQ_NO_PP
-  // one 8-wave workgroup per query block once every CU gets one
-  if (be == 256 && bh * (sq / 256) >= 256 && (D == 128 || D == 64) &&
+  // one 8-wave workgroup per query block once every CU gets one, at head dim
+  // 128; at head dim 64 the 4-wave kernel is faster (block 256, 40 960 tokens,
+  // 24 heads: 1.98 against 2.03 ms at topk 20, 1.02 against 1.08 at topk 10;
+  // at head dim 128 the 8-wave kernel leads, 4.92 against 5.85 ms)
+  if (be == 256 && bh * (sq / 256) >= 256 && D == 128 &&
       (dtype == VSA_BF16 || dtype == VSA_F16)) {
-#define VSA_DQ_PP(TT, DD)                                                                    \
-  launch_dq_pp<TT, DD>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, q_vbs, bh, sq, \
-                       skv, topk, scale, s)
-    if (dtype == VSA_BF16) return D == 128 ? VSA_DQ_PP(__bf16, 128) : VSA_DQ_PP(__bf16, 64);
-    return D == 128 ? VSA_DQ_PP(_Float16, 128) : VSA_DQ_PP(_Float16, 64);
-#undef VSA_DQ_PP
+    if (dtype == VSA_BF16)
+      return launch_dq_pp<__bf16, 128>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c,
+                                        q_vbs, bh, sq, skv, topk, scale, s);
+    return launch_dq_pp<_Float16, 128>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c,
+                                        q_vbs, bh, sq, skv, topk, scale, s);
   }
 #endif
 #define VSA_DQ_CASE(DD, BB)                                                                  \
@@ -1405,7 +1407,7 @@ extern "C" int vsa_sparse_bwd_dq_tiled(const void* q, const void* k, const void*
   hipStream_t s = (hipStream_t)stream;
 #define VSA_DQ_TILED_CASE(DD, BB)                                                            \
   if (D == DD && be == BB) {                                                                 \
-    if (BB == 256 && bh * (sq / 256) >= 256)                                                 \
+    if (BB == 256 && DD == 128 && bh * (sq / 256) >= 256)                                    \
       return launch_dq_pp<T, DD, true>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, \
                                        q_vbs, bh, sq, skv, topk, scale, s, slot_rows, s_out, heads); \
     return launch_dq<T, DD, BB, true>(q, k, v, dout, lse, delta, selected, kv_vbs, dq, d_q_c, \

@@ -712,8 +712,12 @@ static int launch_fwd(const void* q, const void* k, const void* v, const int32_t
 using namespace vsa;
 
 #ifndef VSA_FWD_NO_PP
-// one 8-wave workgroup per query block: used once there are enough blocks to
-// give every CU one (smaller grids run better as 4-wave half-block workgroups)
+// one 8-wave workgroup per query block: used at head dim 128 once there are
+// enough blocks to give every CU one (smaller grids run better as 4-wave
+// half-block workgroups).  At head dim 64 the 4-wave kernel is faster at every
+// grid (block 256, 40 960 tokens, 24 heads: 1.53 against 1.87 ms at topk 20,
+// 0.81 against 1.03 at topk 10; at head dim 128 the 8-wave kernel leads, 4.07
+// against 4.40 ms at 40 heads, topk 20).
 #define VSA_FWD_PP_CASE(DD)                                                                    \
   if (D == DD && be == 256 && bh * (sq / 256) >= 256)                                          \
     return launch_fwd_pp<T, DD>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c, gate, gate_mode,   \
@@ -766,7 +770,6 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
                           gate_heads, bh, sq, skv, D, be, topk, scale, s);
   VSA_DISPATCH_MFMA(dtype, T, {
     VSA_FWD_PP_CASE(128)
-    VSA_FWD_PP_CASE(64)
     VSA_FWD_CASE(128, 256)
     VSA_FWD_CASE(128, 128)
     VSA_FWD_CASE(128, 64)
@@ -782,7 +785,7 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
 
 #define VSA_FWD_TILED_CASE(DD, BB)                                                             \
   if (D == DD && be == BB) {                                                                   \
-    if (BB == 256 && bh * (sq / 256) >= 256)                                                   \
+    if (BB == 256 && DD == 128 && bh * (sq / 256) >= 256)                                      \
       return launch_fwd_pp<T, DD, true>(q, k, v, selected, kv_vbs, out, fine_out, lse, out_c,  \
                                         gate, gate_mode, 0, bh, sq, skv, topk, scale, s,       \
                                         slot_rows, s_out, heads);                                     \
