@@ -77,6 +77,28 @@ def _events_time(fn, iters):
     return start.elapsed_time(end) / iters
 
 
+def _timed_steps(fn, steps):
+    """Run ``fn`` ``steps`` times between two device synchronisations.
+    Returns (mean ms per step from the host clock around the whole run, median
+    ms per step from HIP events recorded between consecutive steps on the
+    launch stream; recording them adds no synchronisation)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    marks[0].record(stream)
+    for i in range(steps):
+        fn()
+        marks[i + 1].record(stream)
+    torch.cuda.synchronize()
+    mean = (time.perf_counter() - t0) * 1e3 / steps
+    per = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(steps))
+    mid = steps // 2
+    median = per[mid] if steps % 2 else 0.5 * (per[mid - 1] + per[mid])
+    return mean, median
+
+
 def host_cpu():
     """The host CPU the baseline runs on: model, logical CPUs of the machine and
     of this process, and the physical cores among this process's CPUs."""
@@ -200,15 +222,12 @@ def run_workload(key, steps, warmup):
     step()
     torch.cuda.synchronize()
     peak = torch.cuda.max_memory_allocated() - base
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms, ms_median = _timed_steps(step, steps)
     fms = _events_time(fwd_only, max(5, steps // 2))
     F = flops_fwd(B, H, S, D, be, topk)   # padded volume, selected pairs only
     return {"workload": key, "name": w["name"], "dtype": w.get("dtype", "bf16"),
-            "ms_fwd_bwd": round(ms, 3), "ms_fwd": round(fms, 3),
+            "ms_fwd_bwd": round(ms, 3), "ms_fwd_bwd_median": round(ms_median, 3),
+            "ms_fwd": round(fms, 3),
             "tflops_fwd_bwd": round(3.5 * F / (ms * 1e-3) / 1e12, 1),
             "tflops_fwd": round(F / (fms * 1e-3) / 1e12, 1),
             "pct_bf16_peak_fwd_bwd": round(100 * 3.5 * F / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 2),
@@ -466,12 +485,7 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_step, ms_median = _timed_steps(step, args.steps)
     fwd_ms = _events_time(fwd_only, max(5, args.steps // 2))
 
     # ---- per-kernel timings (HIP events on the launch stream) -------------
@@ -504,24 +518,29 @@ def main():
         it = 10
         kt = {
             "pool_qkv": (_events_time(lambda: M.block_mean_qkv(qd, kd, vd, vbs, vbs, be), it),
-                         None),
+                         None, None),
             "coarse_fwd_topk": (_events_time(lambda: M.coarse_forward(qc, kc, vc, topk, scale), it),
-                                None),
+                                None, None),
             "sparse_fwd": (_events_time(lambda: M.sparse_forward(qd, kd, vd, sel, vbs, be, scale,
                                                                  out_c=outc, gate=gd), it),
-                           F_fwd),
+                           F_fwd, F_fwd),
             "bwd_prep": (_events_time(lambda: M.backward_prep(fine, do, be, out_c=outc, gate=gd),
-                                      it), None),
+                                      it), None, None),
             "coarse_bwd": (_events_time(lambda: M.coarse_backward(qc, kc, vc, probs, d_outc,
-                                                                  scale), it), None),
-            "csr_build": (_events_time(lambda: M.invert_routes(sel, nb), it), None),
-            "sparse_bwd_dq": (_events_time(k_dq, it), 1.5 * F_fwd),
-            "sparse_bwd_dkdv": (_events_time(k_dkdv, it), 1.0 * F_fwd),
+                                                                  scale), it), None, None),
+            "csr_build": (_events_time(lambda: M.invert_routes(sel, nb), it), None, None),
+            # attributed (the 2.5 F_fwd backward split 1.5 / 1.0) and executed FLOPs:
+            # dK/dV recomputes S and dP (2 of its 4 products)
+            "sparse_bwd_dq": (_events_time(k_dq, it), 1.5 * F_fwd, 1.5 * F_fwd),
+            "sparse_bwd_dkdv": (_events_time(k_dkdv, it), 1.0 * F_fwd, 2.0 * F_fwd),
         }
-    kernels = {n: {"ms": round(t, 4)} for n, (t, _) in kt.items()}
-    for n, (t, f) in kt.items():
+    kernels = {n: {"ms": round(t, 4)} for n, (t, _, _) in kt.items()}
+    for n, (t, f, fx) in kt.items():
         if f:
             kernels[n]["tflops_algorithmic"] = round(f / (t * 1e-3) / 1e12, 1)
+            kernels[n]["tflops_executed"] = round(fx / (t * 1e-3) / 1e12, 1)
+            kernels[n]["frac_bf16_peak_executed"] = round(fx / (t * 1e-3) / 1e12
+                                                          / MFMA_BF16_PEAK_TFLOPS, 4)
     # the bandwidth kernels against the HBM peak, on the bytes each must move
     # once: pooling reads q, k, v and writes the block means; bwd_prep (delta and
     # the combine backward) reads the fine output, dO and the gate and writes
@@ -536,7 +555,7 @@ def main():
         kernels[n]["gbs_algorithmic"] = round(gbs, 1)
         kernels[n]["frac_hbm_peak"] = round(gbs / HBM_PEAK_GBS, 3)
     dom = max((n for n in kt if kt[n][1]), key=lambda n: kt[n][0])
-    dom_t, dom_f = kt[dom]
+    dom_t, dom_f, _ = kt[dom]
     achieved = dom_f / (dom_t * 1e-3) / 1e12
 
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
@@ -559,7 +578,8 @@ def main():
         workloads = {}
         for key in ("c2", "c3tok", "c4", "c5"):
             r = run_workload(key, args.workload_steps, 2)
-            workloads[key] = {n: r[n] for n in ("ms_fwd_bwd", "ms_fwd", "tflops_fwd_bwd",
+            workloads[key] = {n: r[n] for n in ("ms_fwd_bwd", "ms_fwd_bwd_median", "ms_fwd",
+                                                "tflops_fwd_bwd",
                                                 "tflops_fwd", "pct_bf16_peak_fwd_bwd",
                                                 "peak_hbm_gib_beyond_inputs", "steps")}
             torch.cuda.empty_cache()
@@ -583,6 +603,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(ms_median, 4),
         "fwd_ms": round(fwd_ms, 4),
         "bwd_ms": round(ms_step - fwd_ms, 4),
         "pct_bf16_peak": round(100 * value / MFMA_BF16_PEAK_TFLOPS, 2),

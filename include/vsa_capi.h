@@ -67,7 +67,8 @@ enum vsa_status {
   VSA_ERR_UNSUPPORTED = -4, /* (block_elements, head_dim) pair has no kernel */
   VSA_ERR_LAUNCH = -5,      /* the HIP launch itself failed */
   VSA_ERR_TOO_LARGE = -6,   /* beyond the static scratch of a no-allocation entry point */
-  VSA_ERR_ALIGN = -7        /* a pointer is not aligned as the shared rules require */
+  VSA_ERR_ALIGN = -7,       /* a pointer is not aligned as the shared rules require */
+  VSA_ERR_DEVICE = -8       /* the stream belongs to another GPU than the current one */
 };
 
 /* Text for a status code (static storage). */
@@ -241,8 +242,10 @@ int vsa_sparse_bwd_dkdv(const void* q, const void* k, const void* v, const void*
  * (8 * ceil(tiles / 8) + 16 > 262,144 entries, tiles as in
  * vsa_dkdv_tile_order) return VSA_ERR_TOO_LARGE.  Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (two streams, or two host
- * threads) race and must be serialised by the caller.  fp32 inputs need no
- * workspace and run as vsa_sparse_bwd_dkdv with tile_order = NULL.
+ * threads) race and must be serialised by the caller.  The array used is the
+ * current device's, so a non-NULL stream must belong to the current device
+ * (else VSA_ERR_DEVICE, before any launch).  fp32 inputs need no workspace and
+ * run as vsa_sparse_bwd_dkdv with tile_order = NULL.
  */
 int vsa_sparse_bwd_dkdv_noalloc(const void* q, const void* k, const void* v, const void* dout,
                                 const float* lse, const float* delta, const int32_t* counts,

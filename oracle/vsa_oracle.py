@@ -24,11 +24,18 @@ Extra hooks that the reference does not have, for parity testing only:
   driven by exactly the route the GPU chose (Top-K ties are resolved by a
   documented rule on the GPU, while ``torch.topk`` leaves tie order open);
 * ``torch_vsa(..., head_chunk=h)`` evaluates the fine branch ``h`` heads at a
-  time so large configurations fit in host memory (heads are independent).
+  time so large configurations fit in host memory (heads are independent);
+* ``video_sparse_attn(..., selected=...)`` does for the dense oracle what
+  ``selected`` does for ``torch_vsa``;
+* ``gather=`` on ``torch_vsa`` / ``sparse_attention`` picks the fine branch's
+  gather (below).
 
 One deliberate precision difference from ``torch_impl.py``: the fine branch
-gathers from fp32 copies of k and v, so gradients of a key block shared by
-many query blocks accumulate in fp32 (see ``_fine_branch``).
+gathers from fp32 copies of k and v by default, so gradients of a key block
+shared by many query blocks are summed in fp32 and rounded once (see
+``_fine_branch``); ``gather="as_written"`` restates torch_impl.py's own
+``torch.gather`` over the broadcast block view instead, and the tests hold the
+GPU gradients to both.
 """
 
 from __future__ import annotations
@@ -67,8 +74,9 @@ PINNING = {
     "torch_vsa": "== masked-fill video_sparse_attn at 1e-5, full / padded / gate / int block "
                  "(tests/test_torch_vsa.py:12-72); unselected blocks get gradient (89-109); "
                  "fp64 gradcheck; bf16 / fp16 output == T(float(out_c) * float(gate) + out_s) "
-                 "by fp64 brute force (planted: out_c kept in fp32); fp32 gather measured "
-                 "against the T gather of torch_impl.py and fp64 on a Zipf hot-key route",
+                 "by fp64 brute force (planted: out_c kept in fp32); fp32 gather and "
+                 "the as-written torch.gather of torch_impl.py measured against fp64 on a "
+                 "Zipf hot-key route (planted: an indexing gather that sums in T)",
     "sparse_attention_reference": "hot-KV dense per-block softmax (tests/test_helion_vsa.py:332-403); "
                                   "all blocks selected == SDPA; LSE2 == log2 sum exp2 brute force",
     "sparse_attention": "fp64 gradcheck; == torch_vsa fine branch with the same route",
@@ -205,8 +213,13 @@ def topk_reference(scores, topk: int) -> np.ndarray:
 # ----------------------------------------------------------------------------
 
 def video_sparse_attn(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, *,
-                      block_size=64, compress_attn_weight=None, sm_scale=None, return_aux=False):
-    """Full ``q k^T`` masked to the Top-K blocks and valid keys (common.py:200-285)."""
+                      block_size=64, compress_attn_weight=None, sm_scale=None, return_aux=False,
+                      selected: Optional[Tensor] = None):
+    """Full ``q k^T`` masked to the Top-K blocks and valid keys (common.py:200-285).
+
+    ``selected`` (test hook, ``[B, H, Qb, topk]``) replaces the Top-K of the
+    coarse scores (common.py:85-94, 250) so the oracle can follow a route the
+    GPU chose; the block mask is then that route scattered into a bool grid."""
     be = as_block_elements(block_size)
     validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
     b, h, sq, d = q.shape
@@ -215,7 +228,11 @@ def video_sparse_attn(q, k, v, variable_block_sizes, q_variable_block_sizes, top
     vbs = variable_block_sizes.to(q.device)
     qvbs = q_variable_block_sizes.to(q.device)
     coarse_scores, out_c = coarse_branch(q, k, v, vbs, qvbs, be, scale)
-    block_mask = topk_block_mask(coarse_scores, topk)
+    if selected is None:
+        block_mask = topk_block_mask(coarse_scores, topk)
+    else:
+        block_mask = torch.zeros_like(coarse_scores, dtype=torch.bool).scatter_(
+            -1, selected.to(q.device).long(), True)
     token_sel = block_mask.repeat_interleave(be, dim=2).repeat_interleave(be, dim=3)
     kv_valid = valid_token_mask(vbs, be).reshape(skv)
     allowed = token_sel & kv_valid.view(1, 1, 1, skv)
@@ -246,20 +263,47 @@ def _gather_blocks(x: Tensor, block_ids: Tensor, be: int) -> Tensor:
     return blocks[bi, hi, block_ids.long()]
 
 
-def _fine_branch(q, k, v, selected, vbs, be, scale):
+def _gather_blocks_as_written(x: Tensor, block_ids: Tensor, be: int) -> Tensor:
+    """The same ``[B,H,Qb,tk,be,D]`` blocks by the reference's own mechanism
+    (torch_impl.py:33-46): ``torch.gather`` along the key-block axis of the
+    block view broadcast over the query blocks.  Its backward scatters each
+    query block's gradient into that broadcast view in x's dtype, and the
+    expand's backward then sums over the query blocks (fp32 accumulation
+    inside torch's reduction, one rounding to x's dtype at the end)."""
+    b, h, s, d = x.shape
+    qb, tk = block_ids.shape[-2:]
+    blocks = x.reshape(b, h, s // be, be, d)
+    source = blocks.unsqueeze(2).expand(b, h, qb, s // be, be, d)
+    index = block_ids.long().view(b, h, qb, tk, 1, 1).expand(b, h, qb, tk, be, d)
+    return torch.gather(source, 3, index)
+
+
+def _fine_branch(q, k, v, selected, vbs, be, scale, gather: str = "fp32"):
     """Sparse fine branch in fp32 over the valid keys of the selected blocks
-    (torch_impl.py:86-106).  Returns ``(out_s fp32 [B,H,Sq,D], lse2 [B,H,Sq])``."""
+    (torch_impl.py:86-106).  Returns ``(out_s fp32 [B,H,Sq,D], lse2 [B,H,Sq])``.
+
+    ``gather="fp32"`` (the default) gathers from fp32 copies of k and v;
+    ``gather="as_written"`` gathers in T and then promotes, as torch_impl.py:86-87
+    does.  Forward values are identical; the backward differs in where a shared
+    key block's per-query-block gradients are rounded (see below)."""
     b, h, sq, d = q.shape
     qb = sq // be
     tk = selected.shape[-1]
-    # Gather from fp32 copies: forward values are the same as gathering in T
-    # and then promoting (torch_impl.py:86-87), but the backward of the gather
-    # then accumulates the per-query-block gradients of a shared key block in
-    # fp32.  Gathering in T (as torch_impl.py does) makes autograd accumulate
-    # them in bf16, which is off by ~1e-2 relative L2 on hot key blocks with
-    # hundreds of in-edges; the reference's Triton kernels accumulate in fp32.
-    sel_k = _gather_blocks(_acc(k), selected, be)
-    sel_v = _gather_blocks(_acc(v), selected, be)
+    # Gather from fp32 copies by default: the backward then sums the
+    # per-query-block gradients of a shared key block in fp32 and rounds once.
+    # The reference's gather (torch_impl.py:43-46, then .float()) rounds each
+    # query block's contribution to T before that sum; on a Zipf(1.2) route
+    # with a key block of 191 in-edges this puts dk / dv at relative L2 2.4e-3
+    # from fp64 against 1.7e-3 for the fp32 gather
+    # (tests/test_oracle_rounding.py), both far inside the 1e-2 parity bar.
+    if gather == "as_written":
+        sel_k = _acc(_gather_blocks_as_written(k, selected, be))
+        sel_v = _acc(_gather_blocks_as_written(v, selected, be))
+    elif gather == "fp32":
+        sel_k = _gather_blocks(_acc(k), selected, be)
+        sel_v = _gather_blocks(_acc(v), selected, be)
+    else:
+        raise ValueError(f"gather must be 'fp32' or 'as_written', got {gather!r}")
     valid_sel = valid_token_mask(vbs, be)[selected.long()]          # [B,H,Qb,tk,be]
     query = _acc(q.reshape(b, h, qb, be, d))
     keys = sel_k.reshape(b, h, qb, tk * be, d)
@@ -273,11 +317,12 @@ def _fine_branch(q, k, v, selected, vbs, be, scale):
 
 def torch_vsa(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, block_size=64,
               compress_attn_weight=None, *, selected: Optional[Tensor] = None,
-              head_chunk: Optional[int] = None):
+              head_chunk: Optional[int] = None, gather: str = "fp32"):
     """VSA forward, differentiable (torch_impl.py:49-113).
 
     ``selected`` (test hook) replaces the ``scores.topk`` route (torch_impl.py:85);
-    ``head_chunk`` evaluates the fine branch a few heads at a time."""
+    ``head_chunk`` evaluates the fine branch a few heads at a time; ``gather``
+    picks the fine branch's gather (``_fine_branch``)."""
     be = as_block_elements(block_size)
     validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
     b, h, sq, d = q.shape
@@ -289,11 +334,11 @@ def torch_vsa(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, block
         selected = scores.topk(topk, dim=-1).indices
     selected = selected.to(q.device).long()
     if head_chunk is None or head_chunk >= h:
-        out_s, _ = _fine_branch(q, k, v, selected, vbs, be, scale)
+        out_s, _ = _fine_branch(q, k, v, selected, vbs, be, scale, gather)
     else:
         parts = [
             _fine_branch(q[:, i:i + head_chunk], k[:, i:i + head_chunk], v[:, i:i + head_chunk],
-                         selected[:, i:i + head_chunk], vbs, be, scale)[0]
+                         selected[:, i:i + head_chunk], vbs, be, scale, gather)[0]
             for i in range(0, h, head_chunk)
         ]
         out_s = torch.cat(parts, dim=1)
@@ -308,20 +353,23 @@ def torch_vsa(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, block
 # Explicit-route sparse executor contract (vsa/triton_impl.py:358-473, 1583-1652)
 # ----------------------------------------------------------------------------
 
-def sparse_attention_reference(q, k, v, selected, variable_block_sizes, block_elements, scale):
+def sparse_attention_reference(q, k, v, selected, variable_block_sizes, block_elements, scale,
+                               gather: str = "fp32"):
     """Fine branch only, on a caller-supplied route; fp32 output and the base-2
     log-sum-exp ``lse2 = m + log2(l)`` the fine kernels save
     (triton_impl.py:189-192, 352-355)."""
     return _fine_branch(q, k, v, selected.long(), variable_block_sizes.to(q.device),
-                        block_elements, scale)
+                        block_elements, scale, gather)
 
 
-def sparse_attention(q, k, v, selected, variable_block_sizes, *, block_size, sm_scale=None):
+def sparse_attention(q, k, v, selected, variable_block_sizes, *, block_size, sm_scale=None,
+                     gather: str = "fp32"):
     """Differentiable explicit-route oracle, output in the input dtype
     (triton_sparse_attention, triton_impl.py:1626-1652)."""
     be = as_block_elements(block_size)
     scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
-    out, _ = sparse_attention_reference(q, k, v, selected, variable_block_sizes, be, scale)
+    out, _ = sparse_attention_reference(q, k, v, selected, variable_block_sizes, be, scale,
+                                        gather)
     return out.to(q.dtype)
 
 

@@ -615,6 +615,7 @@ extern "C" const char* vsa_status_string(int status) {
     case VSA_ERR_ALIGN:
       return "a pointer is misaligned (16 bytes for element-type and score tensors, 4 for int32 "
              "arrays and lse / delta)";
+    case VSA_ERR_DEVICE: return "the stream belongs to another GPU than the current device";
     default: return "unknown status";
   }
 }
@@ -796,11 +797,14 @@ extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const 
 }
 
 namespace vsa {
+bool combine_f32gate_shape_ok(int64_t bh, int64_t sq, int D, int be, int dtype) {
+  return bh > 0 && bh <= kMaxGridY && be > 0 && sq > 0 && sq % be == 0 && vec_dim_ok(D, dtype);
+}
+
 int combine_f32gate(const void* fine, const void* out_c, const void* gate, int gate_mode,
                     int gate_heads, void* out, int64_t bh, int64_t sq, int D, int be, int dtype,
                     hipStream_t s) {
-  if (bh <= 0 || bh > kMaxGridY || be <= 0 || sq <= 0 || sq % be || !vec_dim_ok(D, dtype))
-    return VSA_ERR_SHAPE;
+  if (!combine_f32gate_shape_ok(bh, sq, D, be, dtype)) return VSA_ERR_SHAPE;
   const int qb = (int)(sq / be);
   VSA_DISPATCH_ALL(dtype, T, {
     hipLaunchKernelGGL((combine_f32gate_kernel<T>), dim3(qb, (unsigned)bh), dim3(256), 0, s,

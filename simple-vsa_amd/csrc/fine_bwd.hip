@@ -1365,6 +1365,15 @@ extern "C" int vsa_sparse_bwd_dkdv_noalloc(const void* q, const void* k, const v
   const int64_t tiles = bh * g.tph * g.nsplit;
   const int64_t order_len = 8 * ((tiles + 7) / 8) + 16;
   if (tiles > (1LL << 30) || order_len > kNoAllocScratchInts) return VSA_ERR_TOO_LARGE;
+  // the scratch is the current device's: the stream must launch there too
+  if (stream != nullptr) {
+    int dev = 0;
+    hipDevice_t sdev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess)
+      return VSA_ERR_LAUNCH;
+    if (sdev != dev) return VSA_ERR_DEVICE;
+  }
   int32_t* order = device_scratch();
   if (order == nullptr) return VSA_ERR_LAUNCH;
   // the order call rewrites every entry the dK/dV kernel reads and zeroes its

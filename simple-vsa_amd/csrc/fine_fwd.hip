@@ -746,6 +746,8 @@ extern "C" int vsa_sparse_fwd(const void* q, const void* k, const void* v,
     const int gm = gate_mode & ~VSA_GATE_F32;
     if (gm < 1 || gm > 3 || !gate) return gm == 0 ? VSA_ERR_SHAPE : VSA_ERR_NULL;
     if (gm == 3 && (gate_heads <= 0 || bh % gate_heads)) return VSA_ERR_SHAPE;
+    // the combine's limits, checked before the fine pass writes anything
+    if (!vsa::combine_f32gate_shape_ok(bh, sq, D, be, dtype)) return VSA_ERR_SHAPE;
     void* fine = fine_out ? fine_out : out;
     int rc = vsa_sparse_fwd(q, k, v, selected, kv_vbs, fine, nullptr, lse, nullptr, nullptr, 0,
                             gate_heads, bh, sq, skv, D, be, topk, scale, dtype, stream);

@@ -71,4 +71,7 @@ namespace vsa {
 int combine_f32gate(const void* fine, const void* out_c, const void* gate, int gate_mode,
                     int gate_heads, void* out, int64_t bh, int64_t sq, int D, int be, int dtype,
                     hipStream_t s);
+// The shape checks combine_f32gate makes, for callers that must reject a call
+// before launching anything else.
+bool combine_f32gate_shape_ok(int64_t bh, int64_t sq, int D, int be, int dtype);
 }  // namespace vsa

@@ -3,8 +3,9 @@
 Public entry points keep the reference's operator API:
 
 * ``mi355x_vsa(q, k, v, variable_block_sizes, q_variable_block_sizes, topk,
-  block_size=64, compress_attn_weight=None)`` -- drop-in for ``torch_vsa`` /
-  ``triton_vsa`` (torch_impl.py:49-57, triton_impl.py:1734-1765);
+  block_size=64, compress_attn_weight=None, *, sm_scale=None, return_aux=False)``
+  -- drop-in for ``torch_vsa`` / ``triton_vsa`` (torch_impl.py:49-57,
+  triton_impl.py:1734-1765) and for ``video_sparse_attn`` (common.py:200-212);
 * ``mi355x_sparse_attention(q, k, v, selected, variable_block_sizes, *,
   block_size, sm_scale=None)`` -- drop-in for ``triton_sparse_attention``
   (triton_impl.py:1626-1652).
@@ -302,16 +303,17 @@ def invert_routes(selected: Tensor, key_blocks: int):
 
 
 def sparse_forward(q, k, v, selected, variable_block_sizes, block_elements, scale, *,
-                   out_c=None, gate=None, want_lse=True):
+                   out_c=None, gate=None, want_lse=True, want_fine=False):
     """Fine forward (+ combine when ``out_c`` is given).  Returns (out, lse, fine):
-    with the combine and ``want_lse``, ``fine`` is the fine output as stored in
-    T, which the backward's delta needs (triton_impl.py:408, 598-700); else
-    ``fine`` is ``out`` (no combine) or None (no backward)."""
+    with the combine and ``want_lse`` (or ``want_fine``), ``fine`` is the fine
+    output as stored in T, which the backward's delta needs (triton_impl.py:408,
+    598-700) and ``return_aux`` reports; else ``fine`` is ``out`` (no combine,
+    ``want_lse``) or None."""
     b, h, sq, d = q.shape
     skv = k.shape[2]
     out = torch.empty_like(q)
     lse = (torch.empty((b, h, sq), device=q.device, dtype=torch.float32) if want_lse else None)
-    fine = torch.empty_like(q) if (want_lse and out_c is not None) else None
+    fine = torch.empty_like(q) if ((want_lse or want_fine) and out_c is not None) else None
     gmode = _gate_mode(gate, d, q.dtype) if out_c is not None else _lib.GATE_NONE
     _lib.call("vsa_sparse_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(selected),
               _lib.ptr(variable_block_sizes), _lib.ptr(out), _lib.ptr(fine), _lib.ptr(lse),
@@ -516,11 +518,13 @@ def mi355x_sparse_executor(block_size):
 
 class _VSA(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, gate, vbs, qvbs, topk_, be, scale):
+    def forward(ctx, q, k, v, gate, vbs, qvbs, topk_, be, scale, aux=None):
         qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
-        _, probs, outc, sel = coarse_forward(qc, kc, vc, topk_, scale)
+        scores, probs, outc, sel = coarse_forward(qc, kc, vc, topk_, scale)
         out, lse, fine = sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
                                         want_lse=True)
+        if aux is not None:
+            aux.update(scores=scores, selected=sel, out_c=outc, fine=fine)
         ctx.save_for_backward(q, k, v, gate, vbs, qvbs, qc, kc, vc, probs, outc, sel, fine, lse)
         ctx.be, ctx.scale = be, scale
         return out
@@ -534,7 +538,7 @@ class _VSA(torch.autograd.Function):
         dqc, dkc, dvc = coarse_backward(qc, kc, vc, probs, d_outc, ctx.scale)
         dq, dk, dv = sparse_backward(q, k, v, dout, lse, delta, sel, vbs, ctx.be, ctx.scale,
                                      dqc=dqc, dkc=dkc, dvc=dvc, q_variable_block_sizes=qvbs)
-        return dq, dk, dv, d_gate, None, None, None, None, None
+        return dq, dk, dv, d_gate, None, None, None, None, None, None
 
 
 def _prepare_gate(gate: Optional[Tensor], q: Tensor) -> Optional[Tensor]:
@@ -572,9 +576,20 @@ def _prepare_gate(gate: Optional[Tensor], q: Tensor) -> Optional[Tensor]:
 
 def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
                q_variable_block_sizes: Tensor, topk: int, block_size=64,
-               compress_attn_weight: Optional[Tensor] = None) -> Tensor:
+               compress_attn_weight: Optional[Tensor] = None, *,
+               sm_scale: Optional[float] = None, return_aux: bool = False):
     """Video Sparse Attention on MI355X: ``out = out_c * gate + out_s``
     (torch_impl.py:49-113), coarse routing by Top-K of the pooled scores.
+
+    The keyword-only arguments are those of ``video_sparse_attn``
+    (common.py:200-212): ``sm_scale`` (default ``1/sqrt(head_dim)``) scales
+    both the coarse scores and the fine branch (common.py:225, 241, 262), and
+    ``return_aux`` also returns ``{"coarse_scores", "block_mask",
+    "out_compress", "out_sparse"}`` (common.py:277-284): the coarse scores in
+    q's dtype ``[B, H, Qb, Kb]``, the routed blocks as a bool mask of that
+    shape, the compression output expanded to every token and the fine output
+    (both ``[B, H, S, D]`` in q's dtype).  The aux tensors are detached: they
+    report what the forward computed and carry no gradient.
 
     Top-K ties are resolved towards the smaller key-block id.  When q, k and v
     are per-head views of token-major [B, S, H, D] tensors the kernels read
@@ -585,37 +600,73 @@ def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
     _check_device_path(q, k, v, be)
     if q.shape[0] * q.shape[1] == 0:
         _prepare_gate(compress_attn_weight, q)  # the same shape checks
-        return _empty_batch(q, k, v, compress_attn_weight)
+        out = _empty_batch(q, k, v, compress_attn_weight)
+        return (out, _empty_aux(q, k, be)) if return_aux else out
     gate = _aligned16(_prepare_gate(compress_attn_weight, q))
     q, k, v = (_aligned16(x) for x in (q, k, v))
-    scale = 1.0 / math.sqrt(q.shape[-1])
+    scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     vbs = _i32(variable_block_sizes, q.device)
     qvbs = _i32(q_variable_block_sizes, q.device)
+    aux = {} if return_aux else None
     with torch.cuda.device(q.device):
-        if _raster_views(q, k, v, gate, be):
+        if aux is None and _raster_views(q, k, v, gate, be):
             from . import tiled
             return tiled.vsa_token_major_views(q, k, v, gate, vbs, qvbs, topk, be, scale)
         pads = _padded(q, k, be)
         if pads is not None:
             kbe, kd, pad_q, pad_k, unpad_out = pads
             gate = pad_q(gate, kd if gate is not None and gate.shape[-1] == q.shape[-1] else 1)
-            return unpad_out(_vsa(pad_q(q), pad_k(k), pad_k(v), gate, vbs, qvbs, topk, kbe,
-                                  scale))
-        return _vsa(q.contiguous(), k.contiguous(), v.contiguous(), gate, vbs, qvbs, topk, be,
-                    scale)
+            out = unpad_out(_vsa(pad_q(q), pad_k(k), pad_k(v), gate, vbs, qvbs, topk, kbe,
+                                 scale, aux))
+            if aux is not None:
+                aux["fine"] = _unpad(aux["fine"], _block_rows(q.shape[2], be, kbe, q.device),
+                                     tuple(q.shape))
+                aux["out_c"] = aux["out_c"][..., :q.shape[-1]]
+        else:
+            out = _vsa(q.contiguous(), k.contiguous(), v.contiguous(), gate, vbs, qvbs, topk,
+                       be, scale, aux)
+    return (out, _aux_dict(aux, q, be)) if return_aux else out
 
 
-def _vsa(q, k, v, gate, vbs, qvbs, topk, be, scale):
-    """The op on kernel-native shapes (contiguous, be and head dim supported)."""
+def _aux_dict(aux: dict, q: Tensor, be: int) -> dict:
+    """``video_sparse_attn``'s aux outputs (common.py:277-284) from the forward's
+    own intermediates: scores (fp32 holding T values) rounded to T exactly, the
+    route scattered into a mask, ``out_c`` expanded to every token of its block
+    (padding tokens included, common.py:192-196) and the stored fine output."""
+    b, h, sq, d = q.shape
+    scores, sel = aux["scores"], aux["selected"]
+    mask = torch.zeros(scores.shape, dtype=torch.bool, device=q.device)
+    mask.scatter_(-1, sel.long(), True)
+    outc = aux["out_c"]
+    expanded = outc.unsqueeze(3).expand(b, h, sq // be, be, d).reshape(b, h, sq, d)
+    return {"coarse_scores": scores.to(q.dtype), "block_mask": mask,
+            "out_compress": expanded, "out_sparse": aux["fine"].detach()}
+
+
+def _empty_aux(q: Tensor, k: Tensor, be: int) -> dict:
+    b, h, sq, d = q.shape
+    kb = k.shape[2] // be
+    return {"coarse_scores": q.new_empty((b, h, sq // be, kb)),
+            "block_mask": torch.zeros((b, h, sq // be, kb), dtype=torch.bool, device=q.device),
+            "out_compress": q.new_empty(q.shape), "out_sparse": q.new_empty(q.shape)}
+
+
+def _vsa(q, k, v, gate, vbs, qvbs, topk, be, scale, aux=None):
+    """The op on kernel-native shapes (contiguous, be and head dim supported).
+    With ``aux`` (a dict) the forward's scores, route, ``out_c`` and fine output
+    are put into it."""
     needs_grad = torch.is_grad_enabled() and (
         q.requires_grad or k.requires_grad or v.requires_grad
         or (gate is not None and gate.requires_grad))
     if needs_grad:
-        return _VSA.apply(q, k, v, gate, vbs, qvbs, topk, be, scale)
+        return _VSA.apply(q, k, v, gate, vbs, qvbs, topk, be, scale, aux)
     qc, kc, vc = block_mean_qkv(q, k, v, vbs, qvbs, be)
-    _, _, outc, sel = coarse_forward(qc, kc, vc, topk, scale)
-    return sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
-                          want_lse=False)[0]
+    scores, _, outc, sel = coarse_forward(qc, kc, vc, topk, scale)
+    out, _, fine = sparse_forward(q, k, v, sel, vbs, be, scale, out_c=outc, gate=gate,
+                                  want_lse=False, want_fine=aux is not None)
+    if aux is not None:
+        aux.update(scores=scores, selected=sel, out_c=outc, fine=fine)
+    return out
 
 
 def mi355x_route(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, block_size=64):

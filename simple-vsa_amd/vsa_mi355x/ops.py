@@ -112,15 +112,18 @@ vsa_fwd.register_autograd(_vsa_backward, setup_context=_vsa_setup)
 
 def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
                q_variable_block_sizes: Tensor, topk: int, block_size=64,
-               compress_attn_weight: Optional[Tensor] = None) -> Tensor:
-    """``vsa_mi355x.mi355x_vsa`` (torch_impl.py:49-57) through the custom ops:
-    the same checks, values and gradients, traceable by torch.compile."""
+               compress_attn_weight: Optional[Tensor] = None, *,
+               sm_scale: Optional[float] = None, return_aux: bool = False):
+    """``vsa_mi355x.mi355x_vsa`` (torch_impl.py:49-57, common.py:200-212) through
+    the custom ops: the same checks, values and gradients, traceable by
+    torch.compile.  ``return_aux`` runs the eager function (a graph break)."""
     be = M.as_block_elements(block_size)
     M.validate_vsa_inputs(q, k, v, variable_block_sizes, q_variable_block_sizes, topk, be)
     M._check_device_path(q, k, v, be)
-    if (q.shape[0] * q.shape[1] == 0 or M._padded(q, k, be) is not None):
+    if (return_aux or q.shape[0] * q.shape[1] == 0 or M._padded(q, k, be) is not None):
         return M.mi355x_vsa(q, k, v, variable_block_sizes, q_variable_block_sizes, topk,
-                            block_size, compress_attn_weight)
+                            block_size, compress_attn_weight, sm_scale=sm_scale,
+                            return_aux=return_aux)
     # contiguous gate: d_gate then has the strides the fake implementation
     # gives it (the eager op returns a token-major gate's gradient as a view)
     gate = M._prepare_gate(compress_attn_weight, q)
@@ -130,7 +133,8 @@ def mi355x_vsa(q: Tensor, k: Tensor, v: Tensor, variable_block_sizes: Tensor,
     qvbs = M._i32(q_variable_block_sizes, q.device)
     save = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad or
                                         (gate is not None and gate.requires_grad))
-    return vsa_fwd(q, k, v, gate, vbs, qvbs, topk, be, 1.0 / math.sqrt(q.shape[-1]), save)[0]
+    scale = float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    return vsa_fwd(q, k, v, gate, vbs, qvbs, topk, be, scale, save)[0]
 
 
 # ---------------------------------------------------------------------------

@@ -71,6 +71,12 @@ def test_entry_points_reject_bad_arguments_without_a_gpu():
     assert lib.vsa_sparse_fwd(p, p, p, p, p, p, None, None, p, p, 3, 3,
                               4, 64, 64, 128, 64, 1, 0.1, 0, None) == -2
     assert lib.vsa_bwd_prep(p, p, p, p, 3, 0, p, p, p, 4, 64, 128, 64, 0, None) == -2
+    # an fp32 gate beside bf16 inputs runs the fine pass, then a combine pass;
+    # the combine's limit (batch * heads <= 65535) is checked before the fine
+    # pass writes anything (with no GPU here a launch would fail with -5)
+    f32_full = _lib.GATE_FULL | _lib.GATE_F32
+    assert lib.vsa_sparse_fwd(p, p, p, p, p, p, p, None, p, p, f32_full, 0,
+                              65536, 64, 64, 128, 64, 1, 0.1, 0, None) == -2
     # no-allocation dK/dV: sizes whose tile order exceeds the 1 MiB static scratch
     # (8 * ceil(tiles / 8) + 16 > 262144 int32) are rejected before any launch
     noalloc = [p] * 14

@@ -101,3 +101,17 @@ def test_no_alloc_dkdv_fp32_runs_the_fp32_kernel():
     ek, ev = _with_workspace(p)
     torch.cuda.synchronize()
     assert torch.equal(dk, ek) and torch.equal(dv, ev)
+
+
+def test_no_alloc_dkdv_head_dim_256_two_calls():
+    """Head dim 256 splits each key tile over two workgroups and takes its tiles
+    from the order by workgroup index (no counters): the same bit-for-bit bar,
+    the second call smaller than the first."""
+    big = _problem(74, be=128, d=256, h=4, nb=24, tk=6, dtype=torch.bfloat16)
+    small = _problem(75, be=256, d=256, h=2, nb=6, tk=3, dtype=torch.bfloat16)
+    for p in (big, small):
+        print(f"no-alloc dK/dV: be {p['be']} d {p['d']} heads {p['bh']} seq {p['s']}", flush=True)
+        dk, dv = _no_alloc(p)
+        ek, ev = _with_workspace(p)
+        torch.cuda.synchronize()
+        assert torch.equal(dk, ek) and torch.equal(dv, ev)
