@@ -29,9 +29,11 @@ struct DqCfg {
   static constexpr int QT = BE >= 128 ? 128 : BE;
   static constexpr int NW = QT / 32;
   static constexpr int NT = NW * 64;
-  // keys per chunk: 32 for (D 128, block 64), so that a 2-wave workgroup's
-  // double buffer is 32 KiB and four workgroups share a CU
-  static constexpr int KC = (D == 128 && BE == 64) ? 32 : 64;
+  // keys per chunk: 32 at block 64, so that a 2-wave workgroup's double buffer
+  // is 32 KiB at head_dim 128 (four workgroups share a CU) and 16 KiB at 64
+  // (twice the resident waves of 64-key chunks: c5 forward 0.88 -> 0.78 ms,
+  // dQ 0.93 -> 0.89 ms)
+  static constexpr int KC = BE == 64 ? 32 : 64;
   static constexpr int NSM = KC / 32;            // 32-key sub-tiles per chunk
   static constexpr int WPE = D == 256 ? 1 : 2;    // waves per SIMD the registers are sized for
   static constexpr int TILE = KC * D;            // one K (or V) chunk, swizzled row-major
@@ -261,6 +263,10 @@ struct DkvCfg {
   static constexpr int NC = 4 * (DH / 32);         // LDS reads of C (dO^T and Q^T tiles)
   static constexpr int NV = 16 * KTL;              // P (and dS) values per lane and item
   static constexpr int L = D > 128 ? 6 : KTL > 1 ? 6 : 12;  // LDS operand lookahead (reads)
+  // Step barrier inside the previous step's dV / dK phase (see dkdv_tile);
+  // at block 64 the operands it keeps live across the step boundary do not fit
+  // the register file, and those kernels keep the barrier at the step's top.
+  static constexpr bool EARLY_BARRIER = BE >= 128;
 };
 
 template <typename T, int D, int BE>
@@ -445,10 +451,33 @@ __device__ __forceinline__ void dkdv_tile(
   };
 
   // Every step copies exactly one item (past the last item it re-copies the
-  // last one into the free stage), so item i+1 has landed once at most NS-3
-  // younger items are in flight.
+  // last one into the free stage).
+  //
+  // Stage protocol (NS = 4 stages, one item each).  Step i runs A(i+1) on the
+  // rows of item i+1 and C(i) on the transposed tiles of item i, and copies
+  // item i+3 into the stage of item i-1.
+  //  * EARLY_BARRIER: the step's workgroup barrier sits inside C(i), KB dV / dK
+  //    products before its end.  Every copy piece of item i+3 is issued before
+  //    it, so waiting until at most PER loads are in flight means item i+2 has
+  //    landed in this wave; the barrier then publishes item i+2 to every wave
+  //    and retires every wave's reads of item i (all issued, and waited for by
+  //    the barrier's lgkmcnt, before it), whose stage step i+1 copies into.
+  //    Right after it the first L operand reads of step i+1 (rows of item
+  //    i+2) are issued, so the last KB products of C(i) cover their LDS
+  //    latency and step i+1 opens with an MFMA (c3 dK/dV 1.5 %, c2 4.6 % less
+  //    time than the barrier at the step's top, bit-identical).
+  //  * otherwise the barrier opens step i: at most PER loads in flight means
+  //    item i+1 has landed, the barrier publishes it and retires the reads of
+  //    item i-1, and the step's first operand reads follow it.
+  constexpr bool EB = C::EARLY_BARRIER;
+  constexpr int KB = KTL > 1 ? 2 : 4;               // C iterations after the early barrier
+  constexpr int VB = EB ? NC - 1 - KB : NC;         // the early barrier follows C iteration VB
+  constexpr int CP0 = EB ? NC / 4 : NC / 2;         // copy pieces over C iterations CP0..CP1
+  constexpr int CP1 = EB ? VB : NC - 1;
+  static_assert(!EB || (VB >= CP0 && L <= NA), "barrier placement");
   f32x16 sA[KTL], pA[KTL], sB[KTL], pB[KTL];
   f32x4 lA[4], dA[4], lB[4], dB[4];
+  V8 preA[L], preB[L];
   Copy cpn;
   if (items <= 0) goto epilogue;
   {
@@ -459,7 +488,7 @@ __device__ __forceinline__ void dkdv_tile(
       for (int p = 0; p < C::PER; ++p) copy_piece(cp, i, p);
     }
     cpn = copy_of(NS - 1 < items ? NS - 1 : items - 1);
-    wait_vmcnt<(NS - 2) * C::PER>();
+    wait_vmcnt<(NS - 2) * C::PER>();   // item 0 landed
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < KTL; ++t) {
@@ -477,22 +506,32 @@ __device__ __forceinline__ void dkdv_tile(
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g) read_stats(0, lA, dA, g);
+    if constexpr (EB) {
+      wait_vmcnt<(NS - 3) * C::PER>();   // item 1 landed
+      __syncthreads();
+#pragma unroll
+      for (int x = 0; x < L; ++x) preA[x] = row_read(1, x & 1, x >> 1);
+    }
   }
 
   {
     // One pipeline step on item i (stage S = i % NS): B(i) between the MFMAs
     // of A(i+1), then C(i).  LDS operands stream with a lookahead of L: rows
-    // of item i+1 for A, then transposed tiles of item i for C, then the
-    // statistics of item i+1.  The copy of item i+NS-1 goes to stage S-1.
+    // of item i+1 for A (the first L of them read by the previous step, in
+    // opc), then transposed tiles of item i for C, then the statistics of
+    // item i+1; after the barrier, the first L rows of item i+2 into opn.
+    // The copy of item i+NS-1 goes to stage S-1.
     auto step = [&](auto stage_c, int it, f32x16 (&sc)[KTL], f32x16 (&pc)[KTL],
                     f32x16 (&sn)[KTL], f32x16 (&pn)[KTL], f32x4 (&lc)[4], f32x4 (&dc)[4],
-                    f32x4 (&ln)[4], f32x4 (&dn)[4]) {
+                    f32x4 (&ln)[4], f32x4 (&dn)[4], V8 (&opc)[L], V8 (&opn)[L]) {
       constexpr int S = decltype(stage_c)::value;
-      constexpr int SN = (S + 1) % NS, SP = (S + NS - 1) % NS;
-      wait_vmcnt<(NS - 3) * C::PER>();
-      // publishes item it+1 to every wave and retires every wave's reads of
-      // item it-1, whose stage the copy below reuses
-      __syncthreads();
+      constexpr int SN = (S + 1) % NS, SNN = (S + 2) % NS, SP = (S + NS - 1) % NS;
+      if constexpr (!EB) {
+        wait_vmcnt<(NS - 3) * C::PER>();
+        // publishes item it+1 to every wave and retires every wave's reads of
+        // item it-1, whose stage the copy below reuses
+        __syncthreads();
+      }
       const Copy cp = cpn;
       V8 op[NA + NC];
       auto issue = [&](int x) {
@@ -507,7 +546,12 @@ __device__ __forceinline__ void dkdv_tile(
         }
       };
 #pragma unroll
-      for (int x = 0; x < L; ++x) issue(x);
+      for (int x = 0; x < L; ++x) {
+        if constexpr (EB)
+          op[x] = opc[x];
+        else
+          issue(x);
+      }
 #pragma unroll
       for (int t = 0; t < KTL; ++t) {
         sn[t] = f32x16{};
@@ -565,13 +609,13 @@ __device__ __forceinline__ void dkdv_tile(
           else
             dvacc[mt][t] = E::mfma32(op[NA + vv], bp[t][j], dvacc[mt][t]);
         }
-        // the copy of item it+NS-1, spread over the second half of the dV / dK
-        // MFMAs, which carries no P / dS arithmetic: a copy stalls its wave on
-        // the address unit, and there the stall overlaps MFMAs only (2 % less
-        // step time than spreading them over the S / dP MFMAs, bit-identical)
+        // the copy of item it+NS-1, spread over C iterations CP0..CP1 (before
+        // an early barrier): a copy stalls its wave on the address unit, and
+        // there it overlaps MFMAs and little P / dS arithmetic (2 % less step
+        // time than over the S / dP MFMAs)
 #pragma unroll
         for (int p = 0; p < C::PER; ++p)
-          if (NC / 2 + (p * (NC / 2)) / C::PER == vv) copy_piece(cp, SP, p);
+          if (CP0 + (p * (CP1 - CP0 + 1)) / C::PER == vv) copy_piece(cp, SP, p);
         if (vv < NC / 2) b_slot(NA + vv);
         if (vv == NC / 2 - 1) {
 #pragma unroll
@@ -579,6 +623,15 @@ __device__ __forceinline__ void dkdv_tile(
             bp[t][1] = pack8<T>(pv[t] + 8);
             bs[t][1] = pack8<T>(dsv[t] + 8);
           }
+        }
+        if (EB && vv == VB) {
+          // see the stage protocol above: publishes item it+2, retires the
+          // reads of item it; then the next step's first operand reads
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<(NS - 3) * C::PER>();
+          __syncthreads();
+#pragma unroll
+          for (int x = 0; x < L; ++x) opn[x] = row_read(SNN, x & 1, x >> 1);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -599,14 +652,14 @@ __device__ __forceinline__ void dkdv_tile(
     static_assert(NS == 4, "the step sequence below is unrolled for NS = 4");
     int it = 0;
     for (; it + 4 <= items; it += 4) {
-      step(I0{}, it, sA, pA, sB, pB, lA, dA, lB, dB);
-      step(I1{}, it + 1, sB, pB, sA, pA, lB, dB, lA, dA);
-      step(I2{}, it + 2, sA, pA, sB, pB, lA, dA, lB, dB);
-      step(I3{}, it + 3, sB, pB, sA, pA, lB, dB, lA, dA);
+      step(I0{}, it, sA, pA, sB, pB, lA, dA, lB, dB, preA, preB);
+      step(I1{}, it + 1, sB, pB, sA, pA, lB, dB, lA, dA, preB, preA);
+      step(I2{}, it + 2, sA, pA, sB, pB, lA, dA, lB, dB, preA, preB);
+      step(I3{}, it + 3, sB, pB, sA, pA, lB, dB, lA, dA, preB, preA);
     }
-    if (it < items) step(I0{}, it, sA, pA, sB, pB, lA, dA, lB, dB);
-    if (it + 1 < items) step(I1{}, it + 1, sB, pB, sA, pA, lB, dB, lA, dA);
-    if (it + 2 < items) step(I2{}, it + 2, sA, pA, sB, pB, lA, dA, lB, dB);
+    if (it < items) step(I0{}, it, sA, pA, sB, pB, lA, dA, lB, dB, preA, preB);
+    if (it + 1 < items) step(I1{}, it + 1, sB, pB, sA, pA, lB, dB, lA, dA, preB, preA);
+    if (it + 2 < items) step(I2{}, it + 2, sA, pA, sB, pB, lA, dA, lB, dB, preA, preB);
   }
 
 epilogue:

@@ -32,9 +32,11 @@ struct FwdCfg {
   static constexpr int QT = BE >= 128 ? 128 : BE;  // queries per workgroup
   static constexpr int NW = QT / 32;               // waves per workgroup
   static constexpr int NT = NW * 64;
-  // keys per chunk: 32 for (D 128, block 64) so that a 2-wave workgroup's
-  // double buffer is 32 KiB and four workgroups share a CU
-  static constexpr int KC = (D == 128 && BE == 64) ? 32 : 64;
+  // keys per chunk: 32 at block 64, so that a 2-wave workgroup's double buffer
+  // is 32 KiB at head_dim 128 (four workgroups share a CU) and 16 KiB at 64
+  // (twice the resident waves of 64-key chunks: c5 forward 0.88 -> 0.78 ms,
+  // dQ 0.93 -> 0.89 ms)
+  static constexpr int KC = BE == 64 ? 32 : 64;
   static constexpr int NSM = KC / 32;              // 32-key sub-tiles per chunk
   // waves per SIMD the registers are sized for: head_dim 256 (Q fragments and
   // O accumulators alone take 192 registers) runs one wave per SIMD
