@@ -239,7 +239,11 @@ struct DkvCfg {
   // keys per wave: 64 at head_dim 64, where the fragments and accumulators of
   // two key tiles fit one wave's 512 registers and each Q / dO operand read
   // from LDS then feeds two MFMAs; 32 above
-  static constexpr int KW = D == 64 ? 64 : 32;
+  // waves per SIMD: two at head_dim 64 with block 64 (32 keys each, one item
+  // per step: the other wave of the SIMD covers a wave's P / dS arithmetic,
+  // which at head_dim 64 is as long as its MFMAs), else one
+  static constexpr int WPE = (D == 64 && BE == 64) ? 2 : 1;
+  static constexpr int KW = (D == 64 && WPE == 1) ? 64 : 32;
   static constexpr int KTL = KW / 32;              // 32-key MFMA tiles per wave
   static constexpr int KT = BE < 4 * KW ? BE : 4 * KW;  // keys per workgroup
   static constexpr int NW = KT / KW;
@@ -252,7 +256,7 @@ struct DkvCfg {
   static constexpr int PER = 2 * TP + 1;           // direct loads per thread per item
   // CSR entries staged in LDS (1024 for one-wave workgroups, so that four of
   // them fit a CU's LDS)
-  static constexpr int SEGMAX = NW == 1 ? 1024 : 2048;
+  static constexpr int SEGMAX = (NW == 1 || WPE > 1) ? 1024 : 2048;
   // dK/dV dims accumulated per workgroup: all of them up to 128; for head_dim
   // 256 two workgroups share a key tile, each computing S and dP over all 256
   // dims and accumulating one 128-dim half of dK and dV (the full accumulators
@@ -419,6 +423,8 @@ __device__ __forceinline__ void dkdv_tile(
   // compiler shares one zero register between them and the S / dP tiles and
   // then moves two dK/dV accumulators aside every step to make room for S/dP
   // (about 16 extra accumulator moves per step, and a spill at head_dim 256).
+  // At two waves per SIMD a wave has 256 registers and every product keeps its
+  // accumulator in VGPRs (no AGPR is pinned).
   f32x16 dkacc[C::DH / 32][KTL], dvacc[C::DH / 32][KTL];
 #pragma unroll
   for (int mt = 0; mt < C::DH / 32; ++mt)
@@ -426,7 +432,7 @@ __device__ __forceinline__ void dkdv_tile(
     for (int t = 0; t < KTL; ++t) {
       dkacc[mt][t] = f32x16{};
       dvacc[mt][t] = f32x16{};
-      asm volatile("" : "+a"(dkacc[mt][t]), "+a"(dvacc[mt][t]));
+      if constexpr (C::WPE == 1) asm volatile("" : "+a"(dkacc[mt][t]), "+a"(dvacc[mt][t]));
     }
 
   auto row_read = [&](int stg, int tilesel, int ks) {
@@ -475,6 +481,92 @@ __device__ __forceinline__ void dkdv_tile(
   constexpr int CP0 = EB ? NC / 4 : NC / 2;         // copy pieces over C iterations CP0..CP1
   constexpr int CP1 = EB ? VB : NC - 1;
   static_assert(!EB || (VB >= CP0 && L <= NA), "barrier placement");
+  if constexpr (C::WPE > 1) {
+    // Two waves per SIMD: step i runs item i start to finish (S and dP, P and
+    // dS, dV and dK) on stage i % NS.  It waits until at most (NS - 2) items
+    // of copies are in flight (item i, copied three steps ahead, has landed),
+    // the barrier publishes item i and retires every wave's reads of item i-1,
+    // and the step copies item i+3 into that stage.
+    if (items > 0) {
+#pragma unroll
+      for (int i = 0; i < NS - 1; ++i) {
+        const Copy cp = copy_of(i < items ? i : items - 1);
+#pragma unroll
+        for (int p = 0; p < C::PER; ++p) copy_piece(cp, i, p);
+      }
+      Copy cpn = copy_of(NS - 1 < items ? NS - 1 : items - 1);
+      auto sstep = [&](auto stage_c, int it) {
+        constexpr int S = decltype(stage_c)::value, SP = (S + NS - 1) % NS;
+        wait_vmcnt<(NS - 2) * C::PER>();
+        __syncthreads();
+        const Copy cp = cpn;
+        f32x4 l4[4], d4[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) read_stats(S, l4, d4, g);
+        f32x16 sacc[KTL], pacc[KTL];
+#pragma unroll
+        for (int t = 0; t < KTL; ++t) {
+          sacc[t] = f32x16{};
+          pacc[t] = f32x16{};
+        }
+#pragma unroll
+        for (int ks = 0; ks < D / 16; ++ks) {
+          const V8 qa = row_read(S, 0, ks), da = row_read(S, 1, ks);
+#pragma unroll
+          for (int t = 0; t < KTL; ++t) {
+            sacc[t] = E::mfma32(qa, kf[t][ks], sacc[t]);
+            pacc[t] = E::mfma32(da, vf[t][ks], pacc[t]);
+          }
+        }
+        // the copy of item it+NS-1, issued while the S / dP products run
+#pragma unroll
+        for (int p = 0; p < C::PER; ++p) copy_piece(cp, SP, p);
+        V8 bp[KTL][2], bs[KTL][2];
+#pragma unroll
+        for (int t = 0; t < KTL; ++t) {
+          float pv[16], dsv[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            pv[e] = fast_exp2(fmaf(sacc[t][e], c2, -l4[e >> 2][e & 3]));
+            dsv[e] = pv[e] * (pacc[t][e] - d4[e >> 2][e & 3]);
+          }
+          bp[t][0] = pack8<T>(pv);
+          bp[t][1] = pack8<T>(pv + 8);
+          bs[t][0] = pack8<T>(dsv);
+          bs[t][1] = pack8<T>(dsv + 8);
+        }
+#pragma unroll
+        for (int vv = 0; vv < NC; ++vv) {
+          const int j = vv / (2 * (C::DH / 32)), mt = (vv >> 1) % (C::DH / 32);
+          const V8 a = tr_read(S, (vv & 1) ? 0 : 1, mt, j);
+#pragma unroll
+          for (int t = 0; t < KTL; ++t) {
+            if (vv & 1)
+              dkacc[mt][t] = E::mfma32(a, bs[t][j], dkacc[mt][t]);
+            else
+              dvacc[mt][t] = E::mfma32(a, bp[t][j], dvacc[mt][t]);
+          }
+        }
+        const int nn = it + NS;
+        cpn = copy_of(nn < items ? nn : items - 1);
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      static_assert(NS == 4, "the step sequence below is unrolled for NS = 4");
+      int it = 0;
+      for (; it + 4 <= items; it += 4) {
+        sstep(I0{}, it);
+        sstep(I1{}, it + 1);
+        sstep(I2{}, it + 2);
+        sstep(I3{}, it + 3);
+      }
+      if (it < items) sstep(I0{}, it);
+      if (it + 1 < items) sstep(I1{}, it + 1);
+      if (it + 2 < items) sstep(I2{}, it + 2);
+    }
+  } else {
   f32x16 sA[KTL], pA[KTL], sB[KTL], pB[KTL];
   f32x4 lA[4], dA[4], lB[4], dB[4];
   V8 preA[L], preB[L];
@@ -661,6 +753,7 @@ __device__ __forceinline__ void dkdv_tile(
     if (it + 1 < items) step(I1{}, it + 1, sB, pB, sA, pA, lB, dB, lA, dA, preB, preA);
     if (it + 2 < items) step(I2{}, it + 2, sA, pA, sB, pB, lA, dA, lB, dB, preA, preB);
   }
+  }
 
 epilogue:
   // ---- epilogue ------------------------------------------------------------
@@ -746,7 +839,7 @@ epilogue:
 // launch; without one, a fixed stride over the range in index order.  Head
 // dim 256 keeps one workgroup per tile (tile_order[i] or the XCD order).
 template <typename T, int D, int BE, bool RASTER>
-__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_dkdv_kernel(
+__global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(DkvCfg<D, BE>::WPE, DkvCfg<D, BE>::WPE))) void sparse_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
@@ -1148,9 +1241,9 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
   const int tph = (int)(skv / C::KT);
   const int64_t tiles = bh * tph * C::NSPLIT;
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
-  // persistent: the workgroups the CUs hold at once (one wave per SIMD), at
+  // persistent: the workgroups the CUs hold at once (WPE waves per SIMD), at
   // most one per tile, a multiple of 8 (the XCD count)
-  const int resident = cu_count() * (4 / C::NW);
+  const int resident = cu_count() * (4 * C::WPE / C::NW);
   const int64_t want = ((tiles + 7) / 8) * 8;
   const int grid = C::NSPLIT > 1 || want < resident ? (int)want : (resident / 8) * 8;
   hipLaunchKernelGGL((sparse_dkdv_kernel<T, D, BE, RASTER>), dim3(grid), dim3(C::NT), 0, stream,
@@ -1254,12 +1347,13 @@ struct DkvGeometry {
 };
 static bool dkdv_geometry(int D, int be, int64_t skv, DkvGeometry& g) {
   if (!((D == 64 || D == 128 || D == 256) && (be == 64 || be == 128 || be == 256))) return false;
-  const int kw = D == 64 ? 64 : 32;                 // DkvCfg<D, BE>::KW
+  const int wpe = (D == 64 && be == 64) ? 2 : 1;    // DkvCfg<D, BE>::WPE
+  const int kw = (D == 64 && wpe == 1) ? 64 : 32;   // DkvCfg<D, BE>::KW
   const int kt = be < 4 * kw ? be : 4 * kw;        // DkvCfg<D, BE>::KT
   g.tph = (int)(skv / kt);
   g.tpb = be / kt;
   g.nsplit = D > 128 ? 2 : 1;
-  g.wg_per_cu = 4 / (kt / kw);                     // one wave per SIMD
+  g.wg_per_cu = 4 * wpe / (kt / kw);
   return true;
 }
 
