@@ -15,6 +15,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "dkdv_cfg.h"
 #include "fine_f32.h"
 #include "vsa_device.h"
 #include "vsa_launch.h"
@@ -234,52 +235,7 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
 // items filled by direct global->LDS loads spread over each step.  Every LDS
 // operand read feeds KTL MFMAs (one per key tile of the wave).
 // ===========================================================================
-template <int D, int BE>
-struct DkvCfg {
-  // keys per wave: 64 at head_dim 64, where the fragments and accumulators of
-  // two key tiles fit one wave's 512 registers and each Q / dO operand read
-  // from LDS then feeds two MFMAs; 32 above
-  // waves per SIMD: two at head_dim 64 with block 64 (32 keys each, one item
-  // per step: the other wave of the SIMD covers a wave's P / dS arithmetic,
-  // which at head_dim 64 is as long as its MFMAs), else one
-  static constexpr int WPE = (D == 64 && BE == 64) ? 2 : 1;
-  static constexpr int KW = (D == 64 && WPE == 1) ? 64 : 32;
-  static constexpr int KTL = KW / 32;              // 32-key MFMA tiles per wave
-  static constexpr int KT = BE < 4 * KW ? BE : 4 * KW;  // keys per workgroup
-  static constexpr int NW = KT / KW;
-  static constexpr int NT = NW * 64;
-  static constexpr int QS = 32;                    // queries per LDS stage
-  static constexpr int TILE = QS * D;              // one Q (or dO) sub-tile, swizzled
-  static constexpr int SUBS = BE / QS;             // sub-tiles per query block
-  static constexpr int NS = 4;                     // LDS ring depth (loop unrolled by NS)
-  static constexpr int TP = TILE / 8 / NT;         // direct loads per thread per tile
-  static constexpr int PER = 2 * TP + 1;           // direct loads per thread per item
-  // CSR entries staged in LDS (1024 for one-wave workgroups, so that four of
-  // them fit a CU's LDS)
-  static constexpr int SEGMAX = (NW == 1 || WPE > 1) ? 1024 : 2048;
-  // dK/dV dims accumulated per workgroup: all of them up to 128; for head_dim
-  // 256 two workgroups share a key tile, each computing S and dP over all 256
-  // dims and accumulating one 128-dim half of dK and dV (the full accumulators
-  // would not fit next to the K and V fragments)
-  static constexpr int DH = D > 128 ? 128 : D;
-  static constexpr int NSPLIT = D / DH;
-  static constexpr int NA = 2 * (D / 16);          // LDS reads of A (Q and dO rows interleaved)
-  static constexpr int NC = 4 * (DH / 32);         // LDS reads of C (dO^T and Q^T tiles)
-  static constexpr int NV = 16 * KTL;              // P (and dS) values per lane and item
-  static constexpr int L = D > 128 ? 6 : KTL > 1 ? 6 : 12;  // LDS operand lookahead (reads)
-  // Step barrier inside the previous step's dV / dK phase (see dkdv_tile);
-  // at block 64 the operands it keeps live across the step boundary do not fit
-  // the register file, and those kernels keep the barrier at the step's top.
-  static constexpr bool EARLY_BARRIER = BE >= 128;
-};
-
-template <typename T, int D, int BE>
-struct DkvShared {
-  using C = DkvCfg<D, BE>;
-  __attribute__((aligned(16))) T smem[C::NS][2 * C::TILE];
-  __attribute__((aligned(16))) float sstat[C::NS][2][C::QS];  // [stage][lse, delta][query]
-  int32_t sseg[C::SEGMAX];
-};
+// DkvCfg (shape, stage protocol) and DkvShared (LDS layout): dkdv_cfg.h
 
 // One key tile (tile_s < num_tiles) of sparse_dkdv_kernel, start to finish.
 // On return every wave's direct loads may still be in flight (the last steps
@@ -367,7 +323,7 @@ __device__ __forceinline__ void dkdv_tile(
   uint32_t cp_goff[TP], cp_loff[TP];  // direct-load pieces: global offset, LDS block
 #pragma unroll
   for (int i = 0; i < TP; ++i) {
-    const int blk = i * (C::NT / 64) + wave;
+    const int blk = C::piece_block(i, wave);
     int c;
     const int row = unswz_row_chunk<D>(blk * 64 + lane, c);
     cp_goff[i] = opaque((uint32_t)((row * D + c * 8) * 2));
@@ -476,11 +432,7 @@ __device__ __forceinline__ void dkdv_tile(
   //    item i+1 has landed, the barrier publishes it and retires the reads of
   //    item i-1, and the step's first operand reads follow it.
   constexpr bool EB = C::EARLY_BARRIER;
-  constexpr int KB = KTL > 1 ? 2 : 4;               // C iterations after the early barrier
-  constexpr int VB = EB ? NC - 1 - KB : NC;         // the early barrier follows C iteration VB
-  constexpr int CP0 = EB ? NC / 4 : NC / 2;         // copy pieces over C iterations CP0..CP1
-  constexpr int CP1 = EB ? VB : NC - 1;
-  static_assert(!EB || (VB >= CP0 && L <= NA), "barrier placement");
+  constexpr int VB = C::VB;   // the early barrier follows C iteration VB
   if constexpr (C::WPE > 1) {
     // Two waves per SIMD: step i runs item i start to finish (S and dP, P and
     // dS, dV and dK) on stage i % NS.  It waits until at most (NS - 2) items
@@ -496,8 +448,8 @@ __device__ __forceinline__ void dkdv_tile(
       }
       Copy cpn = copy_of(NS - 1 < items ? NS - 1 : items - 1);
       auto sstep = [&](auto stage_c, int it) {
-        constexpr int S = decltype(stage_c)::value, SP = (S + NS - 1) % NS;
-        wait_vmcnt<(NS - 2) * C::PER>();
+        constexpr int S = decltype(stage_c)::value, SP = C::copy_stage(S);
+        wait_vmcnt<C::SIMPLE_WAIT>();
         __syncthreads();
         const Copy cp = cpn;
         f32x4 l4[4], d4[4];
@@ -616,10 +568,10 @@ __device__ __forceinline__ void dkdv_tile(
     auto step = [&](auto stage_c, int it, f32x16 (&sc)[KTL], f32x16 (&pc)[KTL],
                     f32x16 (&sn)[KTL], f32x16 (&pn)[KTL], f32x4 (&lc)[4], f32x4 (&dc)[4],
                     f32x4 (&ln)[4], f32x4 (&dn)[4], V8 (&opc)[L], V8 (&opn)[L]) {
-      constexpr int S = decltype(stage_c)::value;
-      constexpr int SN = (S + 1) % NS, SNN = (S + 2) % NS, SP = (S + NS - 1) % NS;
+      constexpr int S = C::c_stage(decltype(stage_c)::value);
+      constexpr int SN = C::a_stage(S), SNN = C::pre_stage(S), SP = C::copy_stage(S);
       if constexpr (!EB) {
-        wait_vmcnt<(NS - 3) * C::PER>();
+        wait_vmcnt<C::STEP_WAIT>();
         // publishes item it+1 to every wave and retires every wave's reads of
         // item it-1, whose stage the copy below reuses
         __syncthreads();
@@ -707,7 +659,7 @@ __device__ __forceinline__ void dkdv_tile(
         // time than over the S / dP MFMAs)
 #pragma unroll
         for (int p = 0; p < C::PER; ++p)
-          if (CP0 + (p * (CP1 - CP0 + 1)) / C::PER == vv) copy_piece(cp, SP, p);
+          if (C::piece_iter(p) == vv) copy_piece(cp, SP, p);
         if (vv < NC / 2) b_slot(NA + vv);
         if (vv == NC / 2 - 1) {
 #pragma unroll
@@ -720,7 +672,7 @@ __device__ __forceinline__ void dkdv_tile(
           // see the stage protocol above: publishes item it+2, retires the
           // reads of item it; then the next step's first operand reads
           __builtin_amdgcn_sched_barrier(0);
-          wait_vmcnt<(NS - 3) * C::PER>();
+          wait_vmcnt<C::STEP_WAIT>();
           __syncthreads();
 #pragma unroll
           for (int x = 0; x < L; ++x) opn[x] = row_read(SNN, x & 1, x >> 1);
@@ -1243,7 +1195,7 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
   if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
   // persistent: the workgroups the CUs hold at once (WPE waves per SIMD), at
   // most one per tile, a multiple of 8 (the XCD count)
-  const int resident = cu_count() * (4 * C::WPE / C::NW);
+  const int resident = cu_count() * C::WG_PER_CU;
   const int64_t want = ((tiles + 7) / 8) * 8;
   const int grid = C::NSPLIT > 1 || want < resident ? (int)want : (resident / 8) * 8;
   hipLaunchKernelGGL((sparse_dkdv_kernel<T, D, BE, RASTER>), dim3(grid), dim3(C::NT), 0, stream,
@@ -1345,16 +1297,25 @@ __global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restr
 struct DkvGeometry {
   int tph, tpb, nsplit, wg_per_cu;
 };
+template <int D, int BE>
+static void dkdv_geometry_of(int64_t skv, DkvGeometry& g) {
+  using C = DkvCfg<D, BE>;
+  g.tph = (int)(skv / C::KT);
+  g.tpb = BE / C::KT;
+  g.nsplit = C::NSPLIT;
+  g.wg_per_cu = C::WG_PER_CU;
+}
 static bool dkdv_geometry(int D, int be, int64_t skv, DkvGeometry& g) {
-  if (!((D == 64 || D == 128 || D == 256) && (be == 64 || be == 128 || be == 256))) return false;
-  const int wpe = (D == 64 && be == 64) ? 2 : 1;    // DkvCfg<D, BE>::WPE
-  const int kw = (D == 64 && wpe == 1) ? 64 : 32;   // DkvCfg<D, BE>::KW
-  const int kt = be < 4 * kw ? be : 4 * kw;        // DkvCfg<D, BE>::KT
-  g.tph = (int)(skv / kt);
-  g.tpb = be / kt;
-  g.nsplit = D > 128 ? 2 : 1;
-  g.wg_per_cu = 4 * wpe / (kt / kw);
-  return true;
+#define VSA_GEO_CASE(DD, BB)            \
+  if (D == DD && be == BB) {            \
+    dkdv_geometry_of<DD, BB>(skv, g);   \
+    return true;                        \
+  }
+  VSA_GEO_CASE(64, 64) VSA_GEO_CASE(64, 128) VSA_GEO_CASE(64, 256)
+  VSA_GEO_CASE(128, 64) VSA_GEO_CASE(128, 128) VSA_GEO_CASE(128, 256)
+  VSA_GEO_CASE(256, 64) VSA_GEO_CASE(256, 128) VSA_GEO_CASE(256, 256)
+#undef VSA_GEO_CASE
+  return false;
 }
 
 }  // namespace vsa

@@ -128,29 +128,29 @@ __device__ __forceinline__ int order_key(float x) {
 // Returns the element offset of the first element of the chunk.
 // ---------------------------------------------------------------------------
 template <int D>
-__device__ __forceinline__ int swz(int r, int c);
+__host__ __device__ __forceinline__ int swz(int r, int c);
 
 template <>
-__device__ __forceinline__ int swz<128>(int r, int c) {
+__host__ __device__ __forceinline__ int swz<128>(int r, int c) {
   return r * 128 + ((c ^ (((r & 3) << 2) | ((r >> 2) & 3))) << 3);
 }
 
 // D = 256: a row is two 128-element halves (256 bytes each, one pass over the
 // 64 banks), each swizzled as a D = 128 row.
 template <>
-__device__ __forceinline__ int swz<256>(int r, int c) {
+__host__ __device__ __forceinline__ int swz<256>(int r, int c) {
   return r * 256 + ((c >> 4) << 7) + (((c & 15) ^ (((r & 3) << 2) | ((r >> 2) & 3))) << 3);
 }
 
 template <>
-__device__ __forceinline__ int swz<64>(int r, int c) {
+__host__ __device__ __forceinline__ int swz<64>(int r, int c) {
   const int R = r >> 1, C = ((r & 1) << 3) | c;
   return R * 128 + ((C ^ (((R & 1) << 2) | ((R >> 1) & 3))) << 3);
 }
 
 // Element offset of X[r][d] for d a multiple of 4 (8-byte aligned pieces).
 template <int D>
-__device__ __forceinline__ int swz_elem(int r, int d) {
+__host__ __device__ __forceinline__ int swz_elem(int r, int d) {
   return swz<D>(r, d >> 3) + (d & 7);
 }
 
@@ -202,24 +202,24 @@ __device__ __forceinline__ typename Elem<T>::vec8 row_a8(const T* X, int row, in
 typedef __attribute__((address_space(3))) void lds_void;
 
 template <int D>
-__device__ __forceinline__ int unswz_row_chunk(int P, int& c);  // P: LDS chunk index
+__host__ __device__ __forceinline__ int unswz_row_chunk(int P, int& c);  // P: LDS chunk index
 
 template <>
-__device__ __forceinline__ int unswz_row_chunk<128>(int P, int& c) {
+__host__ __device__ __forceinline__ int unswz_row_chunk<128>(int P, int& c) {
   const int row = P >> 4;
   c = (P & 15) ^ (((row & 3) << 2) | ((row >> 2) & 3));
   return row;
 }
 
 template <>
-__device__ __forceinline__ int unswz_row_chunk<256>(int P, int& c) {
+__host__ __device__ __forceinline__ int unswz_row_chunk<256>(int P, int& c) {
   const int row = P >> 5, q = P & 31;
   c = (q & 16) | ((q & 15) ^ (((row & 3) << 2) | ((row >> 2) & 3)));
   return row;
 }
 
 template <>
-__device__ __forceinline__ int unswz_row_chunk<64>(int P, int& c) {
+__host__ __device__ __forceinline__ int unswz_row_chunk<64>(int P, int& c) {
   const int R = P >> 4;
   const int C = (P & 15) ^ (((R & 1) << 2) | ((R >> 1) & 3));
   c = C & 7;
