@@ -21,6 +21,8 @@
 // is only moved when a chunk exceeds it by more than 2^kRescaleSlack (the
 // exponentials stay <= 2^8, exact in fp32 and within bf16 range), so the O
 // rescale runs on a few chunks instead of most.
+#include <type_traits>
+
 #include "fine_f32.h"
 #include "vsa_device.h"
 #include "vsa_launch.h"
@@ -310,6 +312,13 @@ struct FwdPPCfg {
   static constexpr int STAGE = 2 * TILE;
   static constexpr int NS = 4;
   static constexpr int PER = 2 * (KC * D / 8 / NT);  // direct loads per wave per chunk
+  // LDS ring: the NS K tiles first, then the NS V tiles.  With the chunk loop
+  // unrolled by NS every operand read is a lane offset (one register, set up
+  // once) plus an immediate below 64 KiB: the K tiles span 64 KiB from 0, and
+  // the V region's start is folded into the transposed-read lane offsets.
+  static constexpr int k_off(int stg) { return stg * TILE; }
+  static constexpr int v_off(int stg) { return (NS + stg) * TILE; }
+  static_assert(D > 128 || NS * TILE * 2 <= 65536, "K tiles addressed by 16-bit offsets");
 };
 
 // One query block (tile < bh * Sq / 256) of sparse_fwd_pp_kernel.
@@ -366,9 +375,8 @@ __device__ __forceinline__ void fwd_pp_tile(
     int nv = 0;
     if (pvalid) {
       const int64_t off = ((int64_t)pkv * BE + pc * C::KC) * D;
-      const uint32_t ks = ring_lds + (uint32_t)(stg * C::STAGE * (int)sizeof(T));
-      tdma.copy_lds(ks, kbase + off, wave);
-      tdma.copy_lds(ks + (uint32_t)(C::TILE * (int)sizeof(T)), vbase + off, wave);
+      tdma.copy_lds(ring_lds + (uint32_t)(C::k_off(stg) * (int)sizeof(T)), kbase + off, wave);
+      tdma.copy_lds(ring_lds + (uint32_t)(C::v_off(stg) * (int)sizeof(T)), vbase + off, wave);
       nv = min(pnvb - pc * C::KC, C::KC);
       ++pc;
       pvalid = route.next(ps, pc, pkv, pnvb);
@@ -387,7 +395,8 @@ __device__ __forceinline__ void fwd_pp_tile(
   // swizzle repeats every 16 rows, so the other rows a lane reads differ from
   // these by constants (instruction offsets): K rows of key 32*smt + r at
   // row_off[ks] + 32*smt*D*2, transposed V pieces of keys 16*kk + .. at
-  // tr_off[mt][hi] + 16*kk*D*2.
+  // tr_off[mt][hi] + 16*kk*D*2.  tr_off also holds the V region's start, so
+  // the V tile of stage s is read at tr_off + k_off(s)*2 + those constants.
   uint32_t row_off[D / 16], tr_off[D / 32][2];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks)
@@ -399,7 +408,7 @@ __device__ __forceinline__ void fwd_pp_tile(
 #pragma unroll
       for (int hi = 0; hi < 2; ++hi)
         tr_off[mt][hi] = opaque((uint32_t)(
-            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3)) *
+            (C::v_off(0) + swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3))) *
             sizeof(T)));
   }
   const char* smem_c = reinterpret_cast<const char*>(smem);
@@ -419,7 +428,7 @@ __device__ __forceinline__ void fwd_pp_tile(
     return as_vec8<T>(rr);
   };
   auto mma_s = [&](int stg) {  // S^T = K Q^T
-    const char* Kb = smem_c + stg * C::STAGE * (int)sizeof(T);
+    const char* Kb = smem_c + C::k_off(stg) * (int)sizeof(T);
     sacc[0] = f32x16{};
     sacc[1] = f32x16{};
 #pragma unroll
@@ -442,11 +451,11 @@ __device__ __forceinline__ void fwd_pp_tile(
 #pragma unroll
       for (int x = 0; x < 32; ++x) tv[x] = sacc[x >> 4][x & 15];
       if (nv < C::KC) {
-        keep_branch();
+        const int nvl = uniform_here(nv);
 #pragma unroll
         for (int x = 0; x < 32; ++x) {
           const int key = (x >> 4) * 32 + 8 * ((x & 15) >> 2) + 4 * h + (x & 3);
-          if (key >= nv) tv[x] = -INFINITY;
+          if (key >= nvl) tv[x] = -INFINITY;
         }
       }
     }
@@ -488,20 +497,18 @@ __device__ __forceinline__ void fwd_pp_tile(
 #pragma unroll
       for (int i = 0; i < 16; ++i) p[smt][i] = fast_exp2(tv[smt * 16 + i]);
     if (nv < C::KC) {
-      keep_branch();
+      const int nvl = uniform_here(nv);
 #pragma unroll
       for (int smt = 0; smt < 2; ++smt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (key >= nv) p[smt][i] = 0.f;
+          if (key >= nvl) p[smt][i] = 0.f;
         }
     }
-    float l4[4] = {0.f, 0.f, 0.f, 0.f};  // chunk row sum in four short chains
+    float l4[4] = {p[0][0], p[0][1], p[0][2], p[0][3]};  // chunk row sum in four short chains
 #pragma unroll
-    for (int smt = 0; smt < 2; ++smt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) l4[i & 3] += p[smt][i];
+    for (int x = 4; x < 32; ++x) l4[x & 3] += p[x >> 4][x & 15];
     lsum += (l4[0] + l4[1]) + (l4[2] + l4[3]);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) pk[kk] = pack8<T>(&p[kk >> 1][8 * (kk & 1)]);
@@ -519,15 +526,15 @@ __device__ __forceinline__ void fwd_pp_tile(
   constexpr int NP = L;  // prefetched operands
   V8 pre[NP];
   auto prefetch = [&](int sj) {
-    const char* Kb = smem_c + sj * C::STAGE * (int)sizeof(T);
+    const char* Kb = smem_c + C::k_off(sj) * (int)sizeof(T);
     __builtin_amdgcn_sched_barrier(0);  // after the softmax phase's arithmetic
 #pragma unroll
     for (int u = 0; u < NP; ++u) pre[u] = k_row(Kb, u >> 1, u & 1);
   };
   static_assert(L <= NSX, "the prefetched operands are K rows");
   auto mma_so = [&](int sj, int sp, int nv) {
-    const char* Kb = smem_c + sj * C::STAGE * (int)sizeof(T);
-    const char* Vb = smem_c + (sp * C::STAGE + C::TILE) * (int)sizeof(T);
+    const char* Kb = smem_c + C::k_off(sj) * (int)sizeof(T);
+    const char* Vb = smem_c + C::k_off(sp) * (int)sizeof(T);  // + tr_off: the V tile
     V8 op[NX];
     auto load = [&](int u) {  // u < NSX: K row (ks = u >> 1, smt = u & 1); else V^T piece
       if (u >= NX) return;
@@ -616,24 +623,36 @@ __device__ __forceinline__ void fwd_pp_tile(
     // group 0 waits for its copies of it before that barrier, group 1, whose
     // copies were issued at the start of the softmax phase just ending, at the
     // end of that phase.  Group 0 prefetches from chunk j+1 right after it.
-    for (int j = 1; nvm1 > 0; ++j) {
+    // The loop is unrolled by NS so that every stage index is a constant.
+    auto iteration = [&](auto jc) {  // chunk j, j % NS == jc
+      constexpr int sj = decltype(jc)::value;
       if (fin > 0) finish(fin);
       if (grp1) dma_wait();  // this wave's copies of chunk j+1
-      prefetch(j % C::NS);
+      prefetch(sj);
       phase_barrier();
       mfma_priority_up();
-      mma_so(j % C::NS, (j - 1) % C::NS, nv0);
+      mma_so(sj, (sj + C::NS - 1) % C::NS, nv0);
       mfma_priority_down();
       if (!grp1) dma_wait();  // this wave's copies of chunk j+1
       phase_barrier();
       // the stage of chunk j+2 last held chunk j-2, read for the last time in
       // group 1's MFMA phase of chunk j-1, which ended before this iteration's
       // first barrier
-      nv2 = issue((j + 2) % C::NS);
+      nv2 = issue((sj + 2) % C::NS);
       fin = nv0;
       nvm1 = nv0;
       nv0 = nv1;
       nv1 = nv2;
+    };
+    static_assert(C::NS == 4, "the unrolled loop below walks four stages");
+    while (nvm1 > 0) {
+      iteration(std::integral_constant<int, 1>{});
+      if (nvm1 <= 0) break;
+      iteration(std::integral_constant<int, 2>{});
+      if (nvm1 <= 0) break;
+      iteration(std::integral_constant<int, 3>{});
+      if (nvm1 <= 0) break;
+      iteration(std::integral_constant<int, 0>{});
     }
   }
   if (!grp1) phase_barrier();

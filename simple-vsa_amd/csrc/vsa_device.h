@@ -261,6 +261,14 @@ __device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32
 // compiler would otherwise drop it and run the selects on every iteration.
 __device__ __forceinline__ void keep_branch() { asm volatile(""); }
 
+// A wave-uniform value redefined at this point: comparisons derived from it
+// inside a rarely taken branch stay in the branch instead of being hoisted
+// (and run on every iteration) in front of it.
+__device__ __forceinline__ int uniform_here(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
 // Keep a lane-dependent value in a register: the compiler would otherwise
 // rematerialise address arithmetic at every use inside a loop.
 template <typename X>
