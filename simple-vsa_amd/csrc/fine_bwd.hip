@@ -159,6 +159,40 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) dqacc[mt] = f32x16{};
 
+  // Per-lane LDS byte offsets inside a tile, set once (the offsets row_a8 /
+  // tr_a8 compute: the swizzle repeats every 16 rows, so rows 32*smt + r sit
+  // at row_off[ks] + 32*smt*D*2 and the transposed pieces of keys 16*kk + ..
+  // at tr_off[mt][hi] + 16*kk*D*2; left to the compiler, that arithmetic was
+  // redone for every chunk).
+  uint32_t row_off[D / 16], tr_off[D / 32][2];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * sizeof(T)));
+  {
+    const int grp = lane >> 4, jl = lane & 15, qq = grp & 1, hh = grp >> 1;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+        tr_off[mt][hi] = opaque((uint32_t)(
+            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3)) * sizeof(T)));
+  }
+  const char* smem_c = reinterpret_cast<const char*>(smem);
+  auto t_row = [&](int stg, int tilesel, int ks, int smt) {  // K (tilesel 0) or V rows 32*smt + r
+    return as_vec8<T>(*reinterpret_cast<const u32x4*>(
+        smem_c + (stg * C::STAGE + tilesel * C::TILE + smt * 32 * D) * (int)sizeof(T) + row_off[ks]));
+  };
+  auto k_tr = [&](int stg, int mt, int kk) {  // K^T pieces, keys 16kk ..
+    const char* base = smem_c + (stg * C::STAGE + kk * 16 * D) * (int)sizeof(T);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][0]));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][1]));
+    u32x4 rr;
+    rr[0] = __builtin_bit_cast(u32x2, lo)[0];
+    rr[1] = __builtin_bit_cast(u32x2, lo)[1];
+    rr[2] = __builtin_bit_cast(u32x2, hi)[0];
+    rr[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return as_vec8<T>(rr);
+  };
+
   RouteRegs<BE, C::KC> route{sel, kv_vbs, topk, kb};
   route.load(0);
   int s = 0, ch = 0, kv = 0, nvb = 0;
@@ -166,14 +200,14 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   if (have) dma(kv, ch, 0);
   dma_wait();
   __syncthreads();
-  int stage = 0;
-  while (have) {
+  // one chunk on stage stg (the loop below is unrolled by the two stages, so
+  // that every LDS address is a lane offset plus an immediate)
+  auto chunk = [&](auto stage_c) {
+    constexpr int stage = decltype(stage_c)::value;
     const int nv = min(nvb - ch * C::KC, C::KC);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
     const bool have2 = route.next(s2, ch2, kv2, nvb2);
     if (have2) dma(kv2, ch2, stage ^ 1);
-    const T* Ks = smem + stage * C::STAGE;
-    const T* Vs = Ks + C::TILE;
 
     f32x16 sacc[C::NSM], pacc[C::NSM];
 #pragma unroll
@@ -182,8 +216,8 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
       for (int smt = 0; smt < C::NSM; ++smt) {
-        sacc[smt] = E::mfma32(row_a8<T, D>(Ks, smt * 32 + r, ks, h), qf[ks], sacc[smt]);
-        pacc[smt] = E::mfma32(row_a8<T, D>(Vs, smt * 32 + r, ks, h), df[ks], pacc[smt]);
+        sacc[smt] = E::mfma32(t_row(stage, 0, ks, smt), qf[ks], sacc[smt]);
+        pacc[smt] = E::mfma32(t_row(stage, 1, ks, smt), df[ks], pacc[smt]);
       }
     }
     // dS^T = P^T (dP^T - delta), consumed 8 keys at a time as the B operand
@@ -197,23 +231,29 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
         dsv[e] = p * (pacc[kk >> 1][i] - my_delta);
       }
       if (nv < C::KC) {
-        keep_branch();
+        // key (kk >> 1)*32 + 8(i >> 2) + (i & 3) + 4h >= nv, compared as 4h >=
+        // nv - (its constant part) on a count re-read inside the branch (no
+        // comparison hoisted out of the branch into every chunk)
+        const int nvl = uniform_here(nv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int i = 8 * (kk & 1) + e;
-          const int key = (kk >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (key >= nv) dsv[e] = 0.f;
+          if (4 * h >= nvl - ((kk >> 1) * 32 + 8 * (i >> 2) + (i & 3))) dsv[e] = 0.f;
         }
       }
       const V8 bop = pack8<T>(dsv);
 #pragma unroll
       for (int mt = 0; mt < D / 32; ++mt)
-        dqacc[mt] = E::mfma32(tr_a8<T, D>(Ks, mt * 32, 16 * kk, 16 * kk + 8), bop, dqacc[mt]);
+        dqacc[mt] = E::mfma32(k_tr(stage, mt, kk), bop, dqacc[mt]);
     }
     dma_wait();
     __syncthreads();
-    stage ^= 1;
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
+  };
+  while (have) {
+    chunk(std::integral_constant<int, 0>{});
+    if (!have) break;
+    chunk(std::integral_constant<int, 1>{});
   }
 
   dq_epilogue<T, D, BE, RASTER>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale, orows,
@@ -1049,12 +1089,14 @@ __device__ __forceinline__ void dq_pp_tile(
         dsv[e] = p * (pacc[kk >> 1][i] - my_delta);
       }
       if (nv < C::KC) {
-        keep_branch();
+        // key (kk >> 1)*32 + 8(i >> 2) + (i & 3) + 4h >= nv, compared as 4h >=
+        // nv - (its constant part) on a count re-read inside the branch (no
+        // comparison hoisted out of the branch into every chunk)
+        const int nvl = uniform_here(nv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int i = 8 * (kk & 1) + e;
-          const int key = (kk >> 1) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (key >= nv) dsv[e] = 0.f;
+          if (4 * h >= nvl - ((kk >> 1) * 32 + 8 * (i >> 2) + (i & 3))) dsv[e] = 0.f;
         }
       }
       bs[kk] = pack8<T>(dsv);

@@ -191,6 +191,40 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
 #pragma unroll
   for (int mt = 0; mt < D / 32; ++mt) oacc[mt] = f32x16{};
 
+  // Per-lane LDS byte offsets inside a tile, set once: the swizzle repeats
+  // every 16 rows, so the K rows of key 32*smt + r sit at row_off[ks] +
+  // 32*smt*D*2 and the transposed V pieces of keys 16*kk + .. at
+  // tr_off[mt][hi] + 16*kk*D*2 (the offsets row_a8 / tr_a8 compute; left to
+  // the compiler, that swizzle arithmetic was redone for every chunk).
+  uint32_t row_off[D / 16], tr_off[D / 32][2];
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * sizeof(T)));
+  {
+    const int grp = lane >> 4, jl = lane & 15, qq = grp & 1, hh = grp >> 1;
+#pragma unroll
+    for (int mt = 0; mt < D / 32; ++mt)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+        tr_off[mt][hi] = opaque((uint32_t)(
+            swz_elem<D>(8 * hi + 4 * hh + (jl >> 2), mt * 32 + 16 * qq + 4 * (jl & 3)) * sizeof(T)));
+  }
+  const char* smem_c = reinterpret_cast<const char*>(smem);
+  auto k_row = [&](int stg, int ks, int smt) {
+    return as_vec8<T>(*reinterpret_cast<const u32x4*>(smem_c + (stg * C::STAGE + smt * 32 * D) * (int)sizeof(T) +
+                                                       row_off[ks]));
+  };
+  auto v_tr = [&](int stg, int mt, int kk) {
+    const char* base = smem_c + (stg * C::STAGE + C::TILE + kk * 16 * D) * (int)sizeof(T);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][0]));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][1]));
+    u32x4 rr;
+    rr[0] = __builtin_bit_cast(u32x2, lo)[0];
+    rr[1] = __builtin_bit_cast(u32x2, lo)[1];
+    rr[2] = __builtin_bit_cast(u32x2, hi)[0];
+    rr[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return as_vec8<T>(rr);
+  };
+
   RouteRegs<BE, C::KC> route{sel, kv_vbs, topk, kb};
   route.load(0);
   int s = 0, ch = 0, kv = 0, nvb = 0;
@@ -198,15 +232,15 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   if (have) dma(kv, ch, 0);
   dma_wait();
   __syncthreads();
-  int stage = 0;
-  while (have) {
+  // one chunk on stage stg (the loop below is unrolled by the two stages, so
+  // that every LDS address is a lane offset plus an immediate)
+  auto chunk = [&](auto stage_c) {
+    constexpr int stage = decltype(stage_c)::value;
     const int nv = min(nvb - ch * C::KC, C::KC);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
     const bool have2 = route.next(s2, ch2, kv2, nvb2);
     if (have2) dma(kv2, ch2, stage ^ 1);  // lands while this chunk is multiplied
 
-    const T* Ks = smem + stage * C::STAGE;
-    const T* Vs = Ks + C::TILE;
     // ---- S^T = K Q^T -------------------------------------------------------
     f32x16 sacc[C::NSM];
 #pragma unroll
@@ -215,18 +249,31 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
       for (int smt = 0; smt < C::NSM; ++smt)
-        sacc[smt] = E::mfma32(row_a8<T, D>(Ks, smt * 32 + r, ks, h), qf[ks], sacc[smt]);
+        sacc[smt] = E::mfma32(k_row(stage, ks, smt), qf[ks], sacc[smt]);
     }
     // ---- online softmax (base 2, lazily rescaled) ---------------------------
+    // Keys past nv get the score -inf.  At head_dim 64 the comparison is 4h >=
+    // nv - (the key's constant part) on a count re-read inside the branch, so
+    // it stays in the (rarely taken) branch: c5 forward -3.6 %.  At head dims
+    // 128 / 256 the compiler hoists the comparisons of the plain form in
+    // front of the branch, under the S products, and that form measured
+    // faster there (t444 forward 7 % faster than with the branch-local one).
     if (nv < C::KC) {
-      keep_branch();
+      if constexpr (D == 64) {
+        const int nvl = uniform_here(nv);
 #pragma unroll
-      for (int smt = 0; smt < C::NSM; ++smt)
+        for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (key >= nv) sacc[smt][i] = -INFINITY;
-        }
+          for (int i = 0; i < 16; ++i)
+            if (4 * h >= nvl - (smt * 32 + 8 * (i >> 2) + (i & 3))) sacc[smt][i] = -INFINITY;
+      } else {
+        keep_branch();
+#pragma unroll
+        for (int smt = 0; smt < C::NSM; ++smt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3) >= nv) sacc[smt][i] = -INFINITY;
+      }
     }
     float m4[4] = {sacc[0][0], sacc[0][1], sacc[0][2], sacc[0][3]};  // short chains
 #pragma unroll
@@ -255,21 +302,26 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) p[smt][i] = fast_exp2(fmaf(sacc[smt][i], c2, negm));
-    if (nv < C::KC) {
-      keep_branch();
+    if (nv < C::KC) {  // as for the scores above
+      if constexpr (D == 64) {
+        const int nvl = uniform_here(nv);
 #pragma unroll
-      for (int smt = 0; smt < C::NSM; ++smt)
+        for (int smt = 0; smt < C::NSM; ++smt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (key >= nv) p[smt][i] = 0.f;
-        }
+          for (int i = 0; i < 16; ++i)
+            if (4 * h >= nvl - (smt * 32 + 8 * (i >> 2) + (i & 3))) p[smt][i] = 0.f;
+      } else {
+        keep_branch();
+#pragma unroll
+        for (int smt = 0; smt < C::NSM; ++smt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (smt * 32 + 8 * (i >> 2) + 4 * h + (i & 3) >= nv) p[smt][i] = 0.f;
+      }
     }
-    float l4[4] = {0.f, 0.f, 0.f, 0.f};  // chunk row sum in four short chains
+    float l4[4] = {p[0][0], p[0][1], p[0][2], p[0][3]};  // chunk row sum in four short chains
 #pragma unroll
-    for (int smt = 0; smt < C::NSM; ++smt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) l4[i & 3] += p[smt][i];
+    for (int x = 4; x < 16 * C::NSM; ++x) l4[x & 3] += p[x >> 4][x & 15];
     lsum += (l4[0] + l4[1]) + (l4[2] + l4[3]);
     // ---- O^T += V^T P^T ------------------------------------------------------
 #pragma unroll
@@ -277,13 +329,17 @@ __global__ __launch_bounds__((FwdCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
       const V8 bop = pack8<T>(&p[kk >> 1][8 * (kk & 1)]);
 #pragma unroll
       for (int mt = 0; mt < D / 32; ++mt)
-        oacc[mt] = E::mfma32(tr_a8<T, D>(Vs, mt * 32, 16 * kk, 16 * kk + 8), bop, oacc[mt]);
+        oacc[mt] = E::mfma32(v_tr(stage, mt, kk), bop, oacc[mt]);
     }
 
     dma_wait();
     __syncthreads();
-    stage ^= 1;
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
+  };
+  while (have) {
+    chunk(std::integral_constant<int, 0>{});
+    if (!have) break;
+    chunk(std::integral_constant<int, 1>{});
   }
 
   fwd_epilogue<T, D, RASTER>(oacc, lsum, m, b, myq, qblk, h, sq, qb, out, fine, lse, outc, gate,
