@@ -199,11 +199,15 @@ int vsa_sparse_bwd_dq(const void* q, const void* k, const void* v, const void* d
  * dK/dV launch walks key blocks in index order (triton_impl.py:1394-1440), and
  * a hot key block (in-edges from most query blocks, as with skewed routes)
  * then serialises the end of the kernel.  The kernel's persistent workgroups
- * take the tiles of their XCD's range in the order written here: longest-first
- * when the range's largest tile exceeds a quarter of an average workgroup
- * slot's share, else index order.  tile_order holds order_len >= 8 * per + 16
- * int32 entries, per = ceil(tiles / 8), tiles = bh * skv / min(block_elements,
- * 128) * (head_dim > 128 ? 2 : 1): the order, then 9 counters this call zeroes
+ * take the tiles of their XCD's range in the order written here, and then
+ * the tiles left in the other XCDs' ranges: longest-first when the range's
+ * largest tile exceeds a quarter of an average workgroup slot's share, else
+ * index order with the range's smallest tiles (at most 4 per workgroup slot)
+ * moved to the end.  tile_order holds order_len >= 8 * per + 16 int32 entries,
+ * per = ceil(tiles / 8), tiles = bh * skv / min(block_elements, head_dim == 64
+ * ? 256 : 128) * (head_dim > 128 ? 2 : 1), below 2^30: the order (entries of
+ * a longest-first range carry bit 30 on top of the tile index; its workgroups
+ * do not take other ranges' tiles), then 9 counters this call zeroes
  * and the dK/dV kernel advances (and leaves zeroed when it ends), so one
  * workspace serves one dK/dV launch at a time.  Results do not depend on the
  * order.

@@ -827,9 +827,17 @@ epilogue:
 // Workgroup i runs on XCD i % 8 and takes tiles from that XCD's contiguous
 // range: with a tile_order workspace (vsa_dkdv_tile_order) the next entry of
 // the range's order comes from the XCD's counter (so early finishers take more
-// tiles) and the last workgroup to finish zeroes the counters for the next
-// launch; without one, a fixed stride over the range in index order.  Head
-// dim 256 keeps one workgroup per tile (tile_order[i] or the XCD order).
+// tiles); once its own range is drained, a workgroup of an index-order range
+// takes the remaining tiles of the other XCDs' ranges (XCD x+1, x+2, ... in
+// turn), since the XCDs do not run equally fast (at c3 some took 3-4 % longer
+// per item than others on the same tile counts: 2.7 % less kernel time with
+// the stealing).  Longest-first ranges (entries tagged kLongestFirst) do not
+// steal: at c5 that cost 1.8 %.  The last workgroup to finish zeroes the
+// counters for the next launch.  Without a workspace, a fixed stride over the
+// range in index order.  Head dim 256 keeps one workgroup per tile
+// (tile_order[i] or the XCD order).
+constexpr int kLongestFirst = 1 << 30;  // tag of the entries of a longest-first range
+
 template <typename T, int D, int BE, bool RASTER>
 __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_per_eu(DkvCfg<D, BE>::WPE, DkvCfg<D, BE>::WPE))) void sparse_dkdv_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -844,7 +852,8 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   if constexpr (DkvCfg<D, BE>::NSPLIT > 1) {
     // head_dim 256: one tile per workgroup (the loop's state would push the
     // fragments and accumulators, which fill the register file, into scratch)
-    const int tile_s = tile_order ? tile_order[blockIdx.x] : xcd_tile(blockIdx.x, num_tiles);
+    const int tile_s = tile_order ? tile_order[blockIdx.x] & (kLongestFirst - 1)
+                                  : xcd_tile(blockIdx.x, num_tiles);
     if (tile_s < num_tiles)
       dkdv_tile<T, D, BE, RASTER>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets,
                                   inverse, kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb,
@@ -856,17 +865,38 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   const int per = (num_tiles + 7) >> 3;       // tiles per XCD range
   const int stride = (int)(gridDim.x >> 3);   // workgroups per XCD
   int32_t* ctr = tile_order ? tile_order + 8 * per : nullptr;  // [8 ranges][done]
+  // (thread 0) ranges xcd .. xcd+from-1 are known to be drained; the ranges
+  // this workgroup may take tiles from end at xcd+last-1
+  int from = 0, last = 1;
   for (int round = 0;; ++round) {
     int j;
     if (ctr) {
-      if (threadIdx.x == 0) s_next = atomicAdd(ctr + xcd, 1);
+      if (threadIdx.x == 0) {
+        int e = per;
+        while (from < last) {
+          // another XCD's counter is read before it is advanced: at the end
+          // every workgroup passes over every drained range, and read-modify-
+          // writes of one address from all of them queue up behind each other
+          int32_t* c = ctr + ((xcd + from) & 7);
+          if (from == 0 || __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < per) {
+            e = atomicAdd(c, 1);
+            if (e < per) break;
+          }
+          ++from;
+        }
+        s_next = from < last ? 8 * e + ((xcd + from) & 7) : -1;  // the order entry
+      }
       __syncthreads();
       j = s_next;
+      if (j < 0) break;
+      // an entry of its own index-order range lets the workgroup steal later
+      if (threadIdx.x == 0 && from == 0 && !(tile_order[j] & kLongestFirst)) last = 8;
     } else {
       j = (int)(blockIdx.x >> 3) + round * stride;
+      if (j >= per) break;
+      j = 8 * j + xcd;
     }
-    if (j >= per) break;
-    const int tile_s = ctr ? tile_order[xcd + 8 * j] : xcd * per + j;
+    const int tile_s = ctr ? tile_order[j] & (kLongestFirst - 1) : xcd * per + (j >> 3);
     if (tile_s < num_tiles)
       dkdv_tile<T, D, BE, RASTER>(sh, tile_s, q, k, v, dout, lse, delta, counts, offsets,
                                   inverse, kv_vbs, dk, dv, dkc, dvc, tiles_per_head, sq, skv, qb,
@@ -1234,7 +1264,7 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
   using C = DkvCfg<D, BE>;
   const int tph = (int)(skv / C::KT);
   const int64_t tiles = bh * tph * C::NSPLIT;
-  if (tiles > (1LL << 30)) return VSA_ERR_SHAPE;
+  if (tiles >= kLongestFirst) return VSA_ERR_SHAPE;  // entries keep the tag bit free
   // persistent: the workgroups the CUs hold at once (WPE waves per SIMD), at
   // most one per tile, a multiple of 8 (the XCD count)
   const int resident = cu_count() * C::WG_PER_CU;
@@ -1251,18 +1281,45 @@ static int launch_dkdv(const void* q, const void* k, const void* v, const void* 
 
 // ---------------------------------------------------------------------------
 // dK/dV tile order.  A dK/dV workgroup's work is proportional to the CSR
-// in-edge count of its key block; on skewed routes (hot key blocks chosen by
-// most query blocks) a few workgroups carry many times the average and, if
-// they start late, set the kernel's end.  One workgroup per XCD range (the
-// tiles xcd_tile gives XCD x) checks whether its largest tile exceeds a
-// quarter of what each concurrent workgroup slot of the XCD gets on average;
-// if so it lists the range longest-first (counting sort on the edge count),
-// else in order.  Workgroup i of the dK/dV grid then takes tile_order[i].
-// Only the dispatch order changes: every tile computes the same values, so
-// the order inside a count bin (set by LDS atomics) does not reach the
-// results.
+// in-edge count of its key block.  One workgroup per XCD range (the tiles
+// xcd_tile gives XCD x) lists the range for the persistent workgroups:
+//  * skewed routes (its largest tile exceeds a quarter of what each concurrent
+//    workgroup slot of the XCD gets on average): longest-first, by a counting
+//    sort on the edge count, so that the hot key blocks start first instead of
+//    setting the kernel's end; these entries carry the kLongestFirst tag;
+//  * otherwise in index order (the two 128-key tiles of a 256-key block, and a
+//    head's neighbouring blocks, which share most query blocks, run together
+//    and meet their Q / dO rows in L2), except that the range's smallest tiles
+//    (at most kTailSlots per workgroup slot) are moved to the end, still in
+//    index order: the last tiles a workgroup takes are then short, and the
+//    workgroups of the XCD finish close together.
+// Workgroup i of the dK/dV grid then takes tile_order[i].  Only the dispatch
+// order changes: every tile computes the same values, so the order inside a
+// count bin (set by LDS atomics) does not reach the results.
 // ---------------------------------------------------------------------------
 constexpr int kOrderBins = 1024;  // edge counts >= 1023 share the top bin
+constexpr int kTailSlots = 4;
+
+// block-wide exclusive prefix sum of one int per thread (1024 threads); the
+// block total is returned in total
+__device__ __forceinline__ int block_exclusive_sum(int v, int* wtot, int& total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  total = 0;
+  for (int w = 0; w < 16; ++w) {
+    if (w < wave) base += wtot[w];
+    total += wtot[w];
+  }
+  __syncthreads();  // wtot may be reused by the next call
+  return base + incl - v;
+}
 
 __global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restrict__ counts,
                                                           int32_t* __restrict__ order,
@@ -1272,6 +1329,8 @@ __global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restr
   __shared__ int bin[kOrderBins];
   __shared__ long long rsum[16];
   __shared__ int rmax[16];
+  __shared__ int wtot[16];
+  __shared__ int s_cut;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int x = blockIdx.x;
   const int lo = x * per, n = max(0, min(per, num_tiles - lo));
@@ -1279,14 +1338,15 @@ __global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restr
   // the finished-workgroup count
   if (tid == 0) order[8 * per + x] = 0;
   if (tid == 0 && x == 0) order[8 * per + 8] = 0;
-  auto nedge_of = [&](int j) {
+  auto nedge_raw = [&](int j) {
     const int tile = (lo + j) / nsplit;
     return counts[(int64_t)(tile / tph) * kb + (tile % tph) / tpb];
   };
+  auto nedge_of = [&](int j) { return min(nedge_raw(j), kOrderBins - 1); };  // its bin
   long long sum = 0;
   int mx = 0;
   for (int j = tid; j < n; j += 1024) {
-    const int e = nedge_of(j);
+    const int e = nedge_raw(j);
     sum += e;
     mx = max(mx, e);
   }
@@ -1299,6 +1359,7 @@ __global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restr
     rmax[wave] = mx;
   }
   bin[tid] = 0;
+  if (tid == 0) s_cut = -1;
   __syncthreads();
   sum = 0;
   mx = 0;
@@ -1306,31 +1367,47 @@ __global__ __launch_bounds__(1024) void dkdv_order_kernel(const int32_t* __restr
     sum += rsum[w];
     mx = max(mx, rmax[w]);
   }
-  if ((long long)mx * slots * 4 <= sum) {
-    for (int j = tid; j < per; j += 1024) order[x + 8 * j] = j < n ? lo + j : num_tiles;
-    return;
-  }
-  for (int j = tid; j < n; j += 1024) atomicAdd(&bin[min(nedge_of(j), kOrderBins - 1)], 1);
+  const bool skewed = (long long)mx * slots * 4 > sum;
+  for (int j = tid; j < n; j += 1024) atomicAdd(&bin[nedge_of(j)], 1);
   __syncthreads();
-  // start of each bin in descending order: sum of the counts of all larger bins
-  const int c = bin[kOrderBins - 1 - tid];  // thread t holds bin K-1-t
-  int incl = c;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
+  // bin[b] becomes the number of tiles with a larger edge count (the start of
+  // bin b in descending order); thread t holds bin K-1-t
+  {
+    const int c = bin[kOrderBins - 1 - tid];
+    int total;
+    const int before = block_exclusive_sum(c, wtot, total);
+    bin[kOrderBins - 1 - tid] = before;
   }
-  __shared__ int wtot[16];
-  if (lane == 63) wtot[wave] = incl;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += wtot[w];
-  bin[kOrderBins - 1 - tid] = base + incl - c;
-  __syncthreads();
-  for (int j = tid; j < n; j += 1024) {
-    const int pos = atomicAdd(&bin[min(nedge_of(j), kOrderBins - 1)], 1);
-    order[x + 8 * pos] = lo + j;
+  if (skewed) {
+    for (int j = tid; j < n; j += 1024) {
+      const int pos = atomicAdd(&bin[nedge_of(j)], 1);
+      order[x + 8 * pos] = (lo + j) | kLongestFirst;
+    }
+  } else {
+    // the cut: the largest edge count c with at most kTailSlots * slots tiles
+    // of count <= c (-1: none, the whole range stays in index order)
+    const int tail_max = kTailSlots * slots;
+    {
+      const int b = tid;
+      const int le = n - bin[b];                                   // tiles with count <= b
+      const int le_next = b + 1 < kOrderBins ? n - bin[b + 1] : n + tail_max + 1;
+      if (le <= tail_max && le_next > tail_max) s_cut = b;
+    }
+    __syncthreads();
+    const int cut = s_cut;
+    const int nbulk = cut < 0 ? n : bin[cut];   // tiles with count > cut
+    int carry = 0;                              // bulk tiles before this chunk
+    for (int j0 = 0; j0 < n; j0 += 1024) {
+      const int j = j0 + tid;
+      const int f = (j < n && nedge_of(j) > cut) ? 1 : 0;
+      int total;
+      const int pre = carry + block_exclusive_sum(f, wtot, total);
+      if (j < n) order[x + 8 * (f ? pre : nbulk + (j - pre))] = lo + j;
+      carry += total;
+    }
   }
-  for (int j = n + tid; j < per; j += 1024) order[x + 8 * j] = num_tiles;
+  for (int j = n + tid; j < per; j += 1024) order[x + 8 * j] = num_tiles | (skewed ? kLongestFirst : 0);
 }
 
 // dK/dV grid geometry of the MFMA kernels for (head_dim, block volume): tiles
@@ -1417,7 +1494,7 @@ extern "C" int vsa_dkdv_tile_order(const int32_t* counts, int32_t* tile_order,
   if (!dkdv_geometry(D, be, skv, g)) return VSA_ERR_UNSUPPORTED;
   const int64_t tiles = bh * g.tph * g.nsplit;
   const int64_t per = (tiles + 7) / 8;
-  if (tiles > (1LL << 30) || order_len < 8 * per + 16) return VSA_ERR_SHAPE;
+  if (tiles >= kLongestFirst || order_len < 8 * per + 16) return VSA_ERR_SHAPE;
   hipLaunchKernelGGL(dkdv_order_kernel, dim3(8), dim3(1024), 0, (hipStream_t)stream, counts,
                      tile_order, (int)tiles, (int)per, g.tph, g.tpb, g.nsplit,
                      (int)(skv / be), 32 * g.wg_per_cu);
@@ -1514,7 +1591,7 @@ extern "C" int vsa_sparse_bwd_dkdv_noalloc(const void* q, const void* k, const v
   if (!dkdv_geometry(D, be, skv, g)) return VSA_ERR_UNSUPPORTED;
   const int64_t tiles = bh * g.tph * g.nsplit;
   const int64_t order_len = 8 * ((tiles + 7) / 8) + 16;
-  if (tiles > (1LL << 30) || order_len > kNoAllocScratchInts) return VSA_ERR_TOO_LARGE;
+  if (tiles >= kLongestFirst || order_len > kNoAllocScratchInts) return VSA_ERR_TOO_LARGE;
   // the scratch is the current device's: the stream must launch there too
   if (stream != nullptr) {
     int dev = 0;

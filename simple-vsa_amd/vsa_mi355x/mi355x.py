@@ -418,8 +418,9 @@ def sparse_backward(q, k, v, dout, lse, delta, selected, variable_block_sizes, b
 def dkdv_tile_order(counts, bh, skv, head_dim, block_elements):
     """Scheduling workspace of the bf16/fp16 dK/dV kernel: each XCD's tile
     range longest-first when one key block's in-edge count would otherwise set
-    the kernel's end (skewed routes), else in order, followed by the counters
-    the persistent workgroups take tiles from (see vsa_dkdv_tile_order)."""
+    the kernel's end (skewed routes), else in index order with the range's
+    smallest tiles last, followed by the counters the persistent workgroups
+    take tiles from (see vsa_dkdv_tile_order)."""
     # keys per workgroup: four waves of 64 keys at head_dim 64, of 32 above
     kt = min(block_elements, 256 if head_dim == 64 else 128)
     tiles = bh * (skv // kt) * (2 if head_dim > 128 else 1)

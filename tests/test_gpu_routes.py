@@ -9,6 +9,7 @@ route is checked against the oracle.  Block 256 at >= 256 query blocks runs the
 8-wave forward, block 64 the 2-wave one."""
 
 import math
+import numpy
 
 import pytest
 import torch
@@ -100,7 +101,9 @@ def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
     per = (tiles + 7) // 8
     assert order.numel() == 8 * per + 16
     assert (order[8 * per:8 * per + 9] == 0).all()           # scheduling counters, reset
-    o = order[:8 * per].cpu().numpy()
+    raw = order[:8 * per].cpu().numpy()
+    tag = 1 << 30                                             # entries of a longest-first range
+    o = raw & (tag - 1)
     real = o[o < tiles]
     assert sorted(real.tolist()) == list(range(tiles))        # every tile exactly once
     assert (o[o >= tiles] == tiles).all()                     # the rest are the sentinel
@@ -110,15 +113,23 @@ def test_dkdv_tile_order_is_a_permutation_and_keeps_results(H, nb, be, D, hot):
     sorted_ranges = 0
     for x in range(8):                                        # each XCD keeps its own range
         ids = o[x::8]
+        tagged = (raw[x::8] & tag) != 0
+        assert tagged.all() or not tagged.any()               # one kind per range
         ids = ids[ids < tiles]
         assert ((ids >= x * per) & (ids < (x + 1) * per)).all()
         rng = nedge[x * per:min((x + 1) * per, tiles)]
         if len(rng) and int(rng.max()) * slots * 4 > int(rng.sum()):   # skewed: longest first
             e = nedge[torch.from_numpy(ids.astype('int64'))]
             assert (e[:-1] >= e[1:]).all()
+            assert tagged.all()
             sorted_ranges += 1
-        else:                                                 # balanced: index order
-            assert (ids == sorted(ids)).all()
+        else:   # balanced: index order, with the smallest tiles (<= 4 per slot) moved last
+            r = rng.clamp(max=1023).numpy()
+            cut = max([c for c in set(r.tolist()) if (r <= c).sum() <= 4 * slots], default=-1)
+            idx = numpy.arange(x * per, x * per + len(r))
+            want = numpy.concatenate([idx[r > cut], idx[r <= cut]])
+            assert (ids == want).all()
+            assert not tagged.any()
     assert sorted_ranges > 0 if hot else True
     # the dispatch order does not reach the results
     P = lambda t: _lib.ptr(t)
