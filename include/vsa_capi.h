@@ -22,8 +22,19 @@
  *  - dtype: VSA_BF16, VSA_F16 or VSA_F32 for every kernel (the fine kernels
  *    run bf16 / fp16 on MFMA and fp32 on fp32 kernels, same results contract);
  *  - nothing here allocates or frees device memory: every output and every
- *    workspace buffer is owned by the caller;
+ *    workspace buffer is owned by the caller (the library's own device memory
+ *    is two file-scope arrays per GPU, held until the process ends: the
+ *    scheduling counters below and vsa_sparse_bwd_dkdv_noalloc's workspace);
  *  - launches are asynchronous on `stream`; no host synchronisation;
+ *  - the persistent forward and dQ kernels (bf16 / fp16, head dim 128, block
+ *    256, at least 256 query blocks) take their query blocks from scheduling
+ *    counters in a slot of a file-scope device array (256 slots of 128 bytes
+ *    per GPU, one per stream that launches them; each launch leaves its slot
+ *    zeroed for the next; a stream that finds every slot taken, or that is
+ *    not on the current device, runs them with a fixed schedule instead, with
+ *    the same results).  Launches on one stream share its slot, which stream
+ *    order keeps apart; a HIP graph captured on stream S holds S's slot, so
+ *    it must not be replayed while launches issued on S itself still run;
  *  - return 0 on success, a negative VSA_ERR_* code otherwise (no exceptions
  *    cross the ABI); vsa_status_string() turns a code into text;
  *  - BH <= 65535 (the per-(batch, head) passes put it in the grid's y

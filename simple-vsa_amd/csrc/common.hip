@@ -2,6 +2,9 @@
 // padded block mean, coarse block attention + Top-K routing, CSR inverse
 // routing, backward preprocessing (delta + combine gradients) and the coarse
 // branch backward.  The MFMA fine kernels live in fine_fwd.hip / fine_bwd.hip.
+#include <mutex>
+#include <unordered_map>
+
 #include "coarse.h"
 #include "vsa_device.h"
 #include "vsa_launch.h"
@@ -593,6 +596,51 @@ __global__ __launch_bounds__(256) void coarse_bwd_cols_kernel(
     d_kc[(b * kb + j) * D + d] = Elem<T>::from_f(ak);
     d_vc[(b * kb + j) * D + d] = Elem<T>::from_f(av);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Scheduling counters of the persistent forward and dQ kernels.  Launches on
+// one stream run one after another, so they can share one slot of counters
+// (each launch's last workgroup zeroes them for the next); launches on
+// different streams may overlap and get different slots.  The array is one
+// copy per GPU, held until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress gives for the current device.
+// ---------------------------------------------------------------------------
+constexpr int kSchedSlots = 256;     // streams per device with a slot of their own
+constexpr int kSchedSlotInts = 32;   // 9 counters, one 128-byte line per slot
+static __device__ __align__(256) int32_t sched_ctr[kSchedSlots * kSchedSlotInts];
+
+namespace {
+std::mutex g_sched_mu;
+int32_t* g_sched_base[64] = {nullptr};
+std::unordered_map<hipStream_t, int> g_sched_slot[64];
+}  // namespace
+
+int32_t* sched_counters(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (s != nullptr) {  // the array used is the current device's
+    hipDevice_t sdev = 0;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess || sdev != dev) return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_sched_mu);
+  if (g_sched_base[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(sched_ctr)) != hipSuccess || p == nullptr)
+      return nullptr;
+    g_sched_base[dev] = static_cast<int32_t*>(p);
+  }
+  auto& slots = g_sched_slot[dev];
+  auto it = slots.find(s);
+  int slot;
+  if (it != slots.end()) {
+    slot = it->second;
+  } else {
+    if ((int)slots.size() >= kSchedSlots) return nullptr;
+    slot = (int)slots.size();
+    slots.emplace(s, slot);
+  }
+  return g_sched_base[dev] + (size_t)slot * kSchedSlotInts;
 }
 
 }  // namespace vsa

@@ -865,27 +865,13 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
   const int per = (num_tiles + 7) >> 3;       // tiles per XCD range
   const int stride = (int)(gridDim.x >> 3);   // workgroups per XCD
   int32_t* ctr = tile_order ? tile_order + 8 * per : nullptr;  // [8 ranges][done]
-  // (thread 0) ranges xcd .. xcd+from-1 are known to be drained; the ranges
-  // this workgroup may take tiles from end at xcd+last-1
+  // (thread 0) the ranges this workgroup may take tiles from: its own, and
+  // with last = 8 the others (take_entry)
   int from = 0, last = 1;
   for (int round = 0;; ++round) {
     int j;
     if (ctr) {
-      if (threadIdx.x == 0) {
-        int e = per;
-        while (from < last) {
-          // another XCD's counter is read before it is advanced: at the end
-          // every workgroup passes over every drained range, and read-modify-
-          // writes of one address from all of them queue up behind each other
-          int32_t* c = ctr + ((xcd + from) & 7);
-          if (from == 0 || __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < per) {
-            e = atomicAdd(c, 1);
-            if (e < per) break;
-          }
-          ++from;
-        }
-        s_next = from < last ? 8 * e + ((xcd + from) & 7) : -1;  // the order entry
-      }
+      if (threadIdx.x == 0) s_next = take_entry(ctr, xcd, per, from, last);  // the order entry
       __syncthreads();
       j = s_next;
       if (j < 0) break;
@@ -904,13 +890,7 @@ __global__ __launch_bounds__((DkvCfg<D, BE>::NT)) __attribute__((amdgpu_waves_pe
     dma_wait();       // this wave's trailing copies land before the LDS is reused
     __syncthreads();  // and every wave is done with it (and with s_next)
   }
-  if (ctr && threadIdx.x == 0) {
-    __threadfence();
-    if (atomicAdd(ctr + 8, 1) == (int)gridDim.x - 1) {
-#pragma unroll
-      for (int x = 0; x < 9; ++x) ctr[x] = 0;
-    }
-  }
+  if (ctr && threadIdx.x == 0) finish_entries(ctr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1199,21 +1179,36 @@ sparse_dq_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
                     const int32_t* __restrict__ kv_vbs, T* __restrict__ dq,
                     const T* __restrict__ dqc, const int32_t* __restrict__ q_vbs, int num_tiles,
                     int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
-                    float scale, const int32_t* __restrict__ orows, int64_t s_out, int heads) {
+                    float scale, const int32_t* __restrict__ orows, int64_t s_out, int heads,
+                    int32_t* __restrict__ ctr) {
   using C = DqPPCfg<D>;
   __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
+  __shared__ int s_next;
   const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
-  for (int j = (int)(blockIdx.x >> 3); j < per; j += stride) {
-    const int tile = xcd * per + j;
-    if (tile >= num_tiles) break;
-    dq_pp_tile<T, D, RASTER>(smem, tile, q, k, v, dout, lse, delta, selected, kv_vbs, dq, dqc,
-                             q_vbs, sq, skv, qb, kb, topk, c2, qsign, scale, orows, s_out, heads);
+  int from = 0;
+  for (int round = 0;; ++round) {
+    int tile;
+    if (ctr) {  // as in sparse_fwd_pp_kernel
+      if (threadIdx.x == 0) s_next = take_entry(ctr, xcd, per, from, 8);
+      __syncthreads();
+      const int e = s_next;
+      if (e < 0) break;
+      tile = (e & 7) * per + (e >> 3);
+    } else {
+      const int j = (int)(blockIdx.x >> 3) + round * stride;
+      if (j >= per) break;
+      tile = xcd * per + j;
+    }
+    if (tile < num_tiles)
+      dq_pp_tile<T, D, RASTER>(smem, tile, q, k, v, dout, lse, delta, selected, kv_vbs, dq, dqc,
+                               q_vbs, sq, skv, qb, kb, topk, c2, qsign, scale, orows, s_out, heads);
     // No copy is in flight here (each chunk's copies are waited for before it
     // is read, and past the route's end nothing is copied): only the
     // epilogue's stores are outstanding, and they drain under the next tile's
     // first loads.
-    __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
+    __syncthreads();  // every wave is done with the LDS ring (and s_next) before the next tile
   }
+  if (ctr && threadIdx.x == 0) finish_entries(ctr);
 }
 
 template <typename T, int D, bool RASTER = false>
@@ -1231,7 +1226,8 @@ static int launch_dq_pp(const void* q, const void* k, const void* v, const void*
                      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, delta, selected,
                      kv_vbs, (T*)dq, (const T*)dqc, q_vbs, (int)tiles, (int)sq, (int)skv,
                      (int)(sq / 256), (int)(skv / 256), topk, fabsf(scale) * kLog2e,
-                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out, heads);
+                     scale < 0.f ? 0x80008000u : 0u, scale, orows, s_out, heads,
+                     sched_counters(stream));
   return vsa_check_launch();
 }
 

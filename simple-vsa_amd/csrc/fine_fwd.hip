@@ -716,10 +716,14 @@ __device__ __forceinline__ void fwd_pp_tile(
                              gate_mode, gate_heads, orows, s_out, heads);
 }
 
-// Persistent: as many workgroups as the CUs hold (one each), every query block
-// has the same topk chunks, so a fixed stride balances them.  Workgroup i runs
-// on XCD i % 8 and walks that XCD's contiguous range of query blocks (the
-// xcd_tile order), so one head's K/V stay in one XCD's L2.
+// Persistent: as many workgroups as the CUs hold (one each).  Workgroup i runs
+// on XCD i % 8 and takes the query blocks of that XCD's contiguous range (the
+// xcd_tile order), so one head's K/V stay in one XCD's L2: with scheduling
+// counters (sched_counters) the next block of the range, then the blocks left
+// in the other XCDs' ranges (take_entry; every block has the same topk chunks,
+// but the XCDs do not run equally fast: 0.6 % less time at c3 and 4.5 % at c4,
+// where 56.25 blocks per workgroup also left a fixed stride uneven); without,
+// a fixed stride over the range.
 template <typename T, int D, bool RASTER>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -727,21 +731,37 @@ sparse_fwd_pp_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
                      T* __restrict__ out, T* __restrict__ fine, float* __restrict__ lse, const T* __restrict__ outc,
                      const T* __restrict__ gate, int gate_mode, int gate_heads, int num_tiles,
                      int sq, int skv, int qb, int kb, int topk, float c2, uint32_t qsign,
-                     const int32_t* __restrict__ orows, int64_t s_out, int heads) {
+                     const int32_t* __restrict__ orows, int64_t s_out, int heads,
+                     int32_t* __restrict__ ctr) {
   using C = FwdPPCfg<D>;
   __shared__ __attribute__((aligned(16))) T smem[C::NS * C::STAGE];
+  __shared__ int s_next;
   const int xcd = blockIdx.x & 7, per = (num_tiles + 7) >> 3, stride = (int)(gridDim.x >> 3);
-  for (int j = (int)(blockIdx.x >> 3); j < per; j += stride) {
-    const int tile = xcd * per + j;
-    if (tile >= num_tiles) break;
-    fwd_pp_tile<T, D, RASTER>(smem, tile, q, k, v, selected, kv_vbs, out, fine, lse, outc, gate,
-                              gate_mode, gate_heads, sq, skv, qb, kb, topk, c2, qsign, orows, s_out, heads);
+  int from = 0;
+  for (int round = 0;; ++round) {
+    int tile;
+    if (ctr) {
+      if (threadIdx.x == 0) s_next = take_entry(ctr, xcd, per, from, 8);
+      __syncthreads();
+      const int e = s_next;
+      if (e < 0) break;
+      tile = (e & 7) * per + (e >> 3);
+    } else {
+      const int j = (int)(blockIdx.x >> 3) + round * stride;
+      if (j >= per) break;
+      tile = xcd * per + j;
+    }
+    if (tile < num_tiles)
+      fwd_pp_tile<T, D, RASTER>(smem, tile, q, k, v, selected, kv_vbs, out, fine, lse, outc, gate,
+                                gate_mode, gate_heads, sq, skv, qb, kb, topk, c2, qsign, orows,
+                                s_out, heads);
     // No copy is in flight here (every chunk's copy is waited for before the
     // chunk is read, and past the route's end nothing is copied), so only the
     // epilogue's stores are outstanding: they drain under the next tile's
     // first loads instead of in front of them.
-    __syncthreads();  // every wave is done with the LDS ring before the next tile's copies
+    __syncthreads();  // every wave is done with the LDS ring (and s_next) before the next tile
   }
+  if (ctr && threadIdx.x == 0) finish_entries(ctr);
 }
 
 template <typename T, int D, bool RASTER = false>
@@ -760,7 +780,8 @@ static int launch_fwd_pp(const void* q, const void* k, const void* v, const int3
   hipLaunchKernelGGL((sparse_fwd_pp_kernel<T, D, RASTER>), dim3(grid), dim3(512), 0, stream,
                      (const T*)q, (const T*)k, (const T*)v, selected, kv_vbs, (T*)out, (T*)fine, lse,
                      (const T*)outc, (const T*)gate, gate_mode, gate_heads, (int)tiles, (int)sq,
-                     (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign, orows, s_out, heads);
+                     (int)skv, (int)(sq / 256), (int)(skv / 256), topk, c2, qsign, orows, s_out, heads,
+                     sched_counters(stream));
   return vsa_check_launch();
 }
 

@@ -515,4 +515,38 @@ __device__ __forceinline__ int xcd_tile(int linear_id, int num_tiles) {
   return (linear_id & 7) * per + (linear_id >> 3);
 }
 
+// Scheduling counters of a persistent kernel's workgroups: ctr[x] hands out
+// the entries 0 .. per-1 of XCD x's range, ctr[8] counts the workgroups that
+// have finished.  Thread 0 of a workgroup on XCD `xcd` takes the next entry of
+// its own range and, once that is drained, of ranges xcd+1 .. xcd+last-1
+// (mod 8): the XCDs do not run equally fast, so the ones that finish first
+// take over the others' remaining tiles.  `from` (kept by the caller from one
+// call to the next, starting at 0) skips the ranges known to be drained.
+// Returns 8 * entry + range, or -1 once every range it may take from is drained.
+__device__ __forceinline__ int take_entry(int32_t* ctr, int xcd, int per, int& from, int last) {
+  while (from < last) {
+    const int x = (xcd + from) & 7;
+    // another range's counter is read before it is advanced: at the end every
+    // workgroup passes over every drained range, and read-modify-writes of one
+    // address from all of them would queue up behind each other
+    if (from == 0 ||
+        __hip_atomic_load(ctr + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < per) {
+      const int e = atomicAdd(ctr + x, 1);
+      if (e < per) return 8 * e + x;
+    }
+    ++from;
+  }
+  return -1;
+}
+
+// Thread 0 of a workgroup that has taken its last entry: the last workgroup to
+// finish zeroes the counters for the next launch.
+__device__ __forceinline__ void finish_entries(int32_t* ctr) {
+  __threadfence();
+  if (atomicAdd(ctr + 8, 1) == (int)gridDim.x - 1) {
+#pragma unroll
+    for (int x = 0; x < 9; ++x) ctr[x] = 0;
+  }
+}
+
 }  // namespace vsa

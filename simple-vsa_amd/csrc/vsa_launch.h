@@ -74,4 +74,10 @@ int combine_f32gate(const void* fine, const void* out_c, const void* gate, int g
 // The shape checks combine_f32gate makes, for callers that must reject a call
 // before launching anything else.
 bool combine_f32gate_shape_ok(int64_t bh, int64_t sq, int D, int be, int dtype);
+// Scheduling counters (take_entry) of the persistent forward and dQ kernels for
+// launches on stream s, from a file-scope device array (common.hip): one slot
+// of zeroed counters per (device, stream), which every launch leaves zeroed.
+// nullptr when the slots are all taken or s is not on the current device: the
+// kernels then use a fixed stride over their XCD's range.
+int32_t* sched_counters(hipStream_t s);
 }  // namespace vsa
