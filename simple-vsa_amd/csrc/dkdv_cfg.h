@@ -52,7 +52,7 @@ struct DkvCfg {
   // LDS of a workgroup (DkvShared with 2-byte elements, plus the persistent
   // loop's tile index) and the workgroups a CU holds at once: WPE waves per
   // SIMD, within the CU's 160 KiB of LDS
-  static constexpr int LDS_BYTES = NS * 2 * TILE * 2 + NS * 2 * QS * 4 + SEGMAX * 4 + 4;
+  static constexpr int LDS_BYTES = NS * 2 * TILE * 2 + NS * 2 * QS * 4 + SEGMAX * 4 + 2 * DH * 2 + 4;
   static constexpr int WG_BY_WAVES = 4 * WPE / NW;
   static constexpr int WG_BY_LDS = 160 * 1024 / LDS_BYTES;
   static constexpr int WG_PER_CU = WG_BY_WAVES < WG_BY_LDS ? WG_BY_WAVES : WG_BY_LDS;
@@ -93,6 +93,9 @@ struct DkvShared {
   __attribute__((aligned(16))) T smem[C::NS][2 * C::TILE];
   __attribute__((aligned(16))) float sstat[C::NS][2][C::QS];  // [stage][lse, delta][query]
   int32_t sseg[C::SEGMAX];
+  // the key block's pooled dK and dV rows (this workgroup's DH dims), divided
+  // by the block's token count and rounded to T: the same for every key
+  __attribute__((aligned(16))) T spool[2][C::DH];
 };
 
 }  // namespace vsa

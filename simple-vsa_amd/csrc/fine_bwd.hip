@@ -335,10 +335,44 @@ __device__ __forceinline__ void dkdv_tile(
   const int nedge = counts[meta];
   const int32_t* seg = inverse + (int64_t)b * qb * topk + offsets[meta];
   const int items = nedge * C::SUBS;
+  // The pooled-gradient rows are one per key block: their dims are divided by
+  // the count and rounded to T here, once per workgroup and dim, into LDS (in
+  // the epilogue every lane would repeat them for its own key: about half of
+  // the epilogue's VALU work).
+  constexpr int NPOOL = (2 * C::DH + C::NT - 1) / C::NT;   // pooled dims per thread
+  float pool_raw[NPOOL];
+  // the thread index passes through an asm that reads the tile, so that the
+  // lane addresses below are formed per tile: hoisted out of the persistent
+  // loop they would stay live (spilled) across every tile
+  int ptid = tid;
+  asm volatile("" : "+v"(ptid) : "s"(tile_s));
+  if (dkc) {
+    const int64_t prow = ((int64_t)b * kb + kvblk) * D + d_off;
+#pragma unroll
+    for (int i = 0; i < NPOOL; ++i) {
+      const int x = ptid + i * C::NT;
+      pool_raw[i] = x < 2 * C::DH ? E::to_f((x < C::DH ? dkc : dvc)[prow + x % C::DH]) : 0.f;
+    }
+  }
+  // The first NT entries of the CSR segment are loaded here too, under the
+  // fragment loads' wait, instead of after it in the first refill (one memory
+  // round trip and a barrier less per tile).
+  const int seg0 = ptid < nedge ? seg[ptid] : 0;
   // Retire the fragment loads before the ring starts: the compiler's own vmcnt
   // bookkeeping does not see the direct loads, and a wait it placed in the
   // loop for these registers would also drain the in-flight stages.
   dma_wait();
+  if (dkc) {
+    const float cdiv = (float)(cnt > 1 ? cnt : 1), rcp = 1.0f / cdiv;
+#pragma unroll
+    for (int i = 0; i < NPOOL; ++i) {
+      const int x = ptid + i * C::NT;
+      if (x < 2 * C::DH)
+        sh.spool[x / C::DH][x % C::DH] = E::from_f(div_by_count(pool_raw[i], cdiv, rcp));
+    }
+  }
+  if (ptid < nedge) sseg[ptid] = seg0;
+  __syncthreads();  // publishes spool and the first CSR entries
   const T* qbase = q + (int64_t)b * sq * D;
   const T* dbase = dout + (int64_t)b * sq * D;
   const float* lbase = lse + (int64_t)b * sq;
@@ -378,8 +412,9 @@ __device__ __forceinline__ void dkdv_tile(
   // item would put scalar-memory latency in front of every copy, a vector
   // load would need vmcnt(0) and drain the ring).  The refill runs where every
   // wave has finished with the previous entries (all waves call qblock_of at
-  // the same program point, between two barriers).
-  int seg_lo = 0, seg_hi = 0;
+  // the same program point, between two barriers).  Entries [0, NT) were
+  // staged before the ring started.
+  int seg_lo = 0, seg_hi = C::NT;
   auto qblock_of = [&](int item) {
     const int e = item / C::SUBS;
     if (e >= seg_hi) {
@@ -749,26 +784,20 @@ __device__ __forceinline__ void dkdv_tile(
 
 epilogue:
   // ---- epilogue ------------------------------------------------------------
-  const float cdiv = (float)(cnt > 1 ? cnt : 1), rcp = 1.0f / cdiv;
-  const T* kcrow = dkc ? dkc + ((int64_t)b * kb + kvblk) * D : nullptr;
-  const T* vcrow = dvc ? dvc + ((int64_t)b * kb + kvblk) * D : nullptr;
-  // The pooled-gradient rows are loaded together before the first store: a
-  // load issued after a store waits for that store too (one in-order vector
-  // memory counter), which made the epilogue 16 store round trips long.
   // every key of the wave is in one key block: one pooled row for all of them
   const bool any_valid = mykey0 - kvblk * BE < nvb;
   // rows regrouped for 16-byte accesses (swap_rows16): w[p][i] is dim
   // d_off + mt*32 + 8(2p + h) + i of this lane's key; both lanes of a swapped
   // pair hold the same key
   u32x4 kcv[C::DH / 32][2], vcv[C::DH / 32][2];
-  if (any_valid && kcrow) {
+  if (any_valid && dkc) {
 #pragma unroll
     for (int mt = 0; mt < C::DH / 32; ++mt)
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const int d0 = d_off + mt * 32 + 16 * p + 8 * h;
-        kcv[mt][p] = *reinterpret_cast<const u32x4*>(kcrow + d0);
-        vcv[mt][p] = *reinterpret_cast<const u32x4*>(vcrow + d0);
+        const int d0 = mt * 32 + 16 * p + 8 * h;   // within this workgroup's dims
+        kcv[mt][p] = *reinterpret_cast<const u32x4*>(&sh.spool[0][d0]);
+        vcv[mt][p] = *reinterpret_cast<const u32x4*>(&sh.spool[1][d0]);
       }
   }
 #pragma unroll
@@ -793,13 +822,13 @@ epilogue:
         const int d0 = d_off + mt * 32 + 16 * p + 8 * h;
         float ck[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         float cv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (key_valid && kcrow) {
+        if (key_valid && dkc) {
           const T* ka = reinterpret_cast<const T*>(&kcv[mt][p]);
           const T* va = reinterpret_cast<const T*>(&vcv[mt][p]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            ck[e] = round_t<T>(div_by_count(E::to_f(ka[e]), cdiv, rcp));
-            cv[e] = round_t<T>(div_by_count(E::to_f(va[e]), cdiv, rcp));
+            ck[e] = E::to_f(ka[e]);
+            cv[e] = E::to_f(va[e]);
           }
         }
         // A padding key gets no gradient; its lane's accumulators (which only
