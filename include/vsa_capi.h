@@ -131,8 +131,10 @@ int vsa_topk(const float* scores, int32_t* selected, int64_t rows,
  * Replaces _invert_indices (triton_impl.py:544-595): counts [BH, Kb],
  * offsets [BH, Kb] (exclusive prefix of counts), inverse [BH, Qb*topk].
  * Unlike the reference's atomic cursor, every segment is written in ascending
- * query-block order, so the result is deterministic.  q_blocks, kv_blocks
- * <= 16000 (one row of counts, and one of query blocks, in LDS).
+ * query-block order, so the result is deterministic (a query block that
+ * chose one key block several times is listed that many times).  q_blocks,
+ * kv_blocks <= 16000 (a bit per query block for each of a workgroup's key
+ * blocks, in LDS).
  */
 int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
                   int32_t* inverse, int64_t bh, int32_t q_blocks, int32_t kv_blocks,

@@ -221,85 +221,149 @@ __global__ __launch_bounds__(256) void coarse_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// CSR inverse routing (triton_impl.py:476-595).
-// Pass 1 (one workgroup per bh): LDS histogram of the route, exclusive scan,
-// counts/offsets out, then an atomic-cursor scatter of query-block ids.
-// Pass 2 (one workgroup per (bh, kv)): put each segment in ascending order by a
-// histogram over query-block ids, which makes the layout deterministic.
+// CSR inverse routing (triton_impl.py:476-595), in one pass without global
+// atomics.  One workgroup per (range of kv_per key blocks, batch-head) marks in
+// LDS which query blocks chose each of its key blocks (bit q of column kv), and
+// counts on the way the edges whose key block lies below its range, which is
+// the range's offset.  A wave per column then counts the column's bits and
+// writes its query-block ids in ascending order, so the layout is
+// deterministic.  (One workgroup per batch-head with LDS-atomic cursors left
+// 24 workgroups at c5, serialised on the hot key blocks' counters.)  A route
+// that chooses one key block twice sets one bit twice: the workgroup notices
+// and lists that range by an ordered scan of the edges instead, so a repeated
+// edge appears as often as it occurs.
 // ---------------------------------------------------------------------------
-__device__ void block_exclusive_scan(int* a, int n, int* tmp256) {
-  // sequential per-thread chunk sums + Hillis-Steele over 256 partials
-  const int per = (n + 255) / 256;
-  const int s0 = threadIdx.x * per;
-  int local = 0;
-  for (int m = 0; m < per && s0 + m < n; ++m) local += a[s0 + m];
-  tmp256[threadIdx.x] = local;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {
-    int add = threadIdx.x >= o ? tmp256[threadIdx.x - o] : 0;
-    __syncthreads();
-    tmp256[threadIdx.x] += add;
-    __syncthreads();
+constexpr int kCsrNT = 512;
+constexpr int kCsrMaxCols = 256;      // key blocks per workgroup
+constexpr int kCsrBitWords = 14336;   // 56 KiB of column bits
+
+// wave-wide inclusive prefix sum
+__device__ __forceinline__ int wave_incl_sum(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(v, o, 64);
+    if (lane >= o) v += y;
   }
-  int run = tmp256[threadIdx.x] - local;
-  for (int m = 0; m < per && s0 + m < n; ++m) {
-    const int c = a[s0 + m];
-    a[s0 + m] = run;
-    run += c;
-  }
-  __syncthreads();
+  return v;
 }
 
-__global__ __launch_bounds__(256) void csr_scatter_kernel(
-    const int32_t* __restrict__ selected, int32_t* __restrict__ counts,
-    int32_t* __restrict__ offsets, int32_t* __restrict__ inverse, int qb, int kb, int topk) {
-  extern __shared__ int ismem[];
-  int* cur = ismem;        // kb: counts, then (after the scan) the write cursors
-  int* tmp = cur + kb;     // 256
-  const int64_t b = blockIdx.x;
+__global__ __launch_bounds__(kCsrNT) void csr_cols_kernel(const int32_t* __restrict__ selected,
+                                                          int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ offsets,
+                                                          int32_t* __restrict__ inverse, int qb,
+                                                          int kb, int topk, int kv_per) {
+  extern __shared__ uint32_t cbits[];  // [nk][qw]
+  __shared__ int ccount[kCsrMaxCols];
+  __shared__ int wpart[kCsrNT / 64];
+  __shared__ int s_dup;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NW = kCsrNT / 64;
+  const int qw = (qb + 31) >> 5;
+  const int64_t b = blockIdx.y;
+  const int kv0 = (int)blockIdx.x * kv_per;
+  const int nk = min(kb - kv0, kv_per);
   const int edges = qb * topk;
   const int32_t* sel = selected + b * edges;
-  for (int j = threadIdx.x; j < kb; j += 256) cur[j] = 0;
+  int32_t* inv = inverse + b * edges;
+  for (int i = tid; i < nk * qw; i += kCsrNT) cbits[i] = 0;
+  for (int i = tid; i < nk; i += kCsrNT) ccount[i] = 0;
+  if (tid == 0) s_dup = 0;
   __syncthreads();
-  for (int e = threadIdx.x; e < edges; e += 256) {
+  int below = 0, dup = 0;
+  for (int e = tid; e < edges; e += kCsrNT) {
     const int kv = sel[e];
-    if (kv >= 0 && kv < kb) atomicAdd(&cur[kv], 1);
+    if (kv < 0 || kv >= kb) continue;  // ids outside [0, kb) contribute nothing
+    if (kv < kv0) {
+      ++below;
+    } else if (kv < kv0 + nk) {
+      const int q = e / topk;
+      const uint32_t bit = 1u << (q & 31);
+      if (atomicOr(&cbits[(kv - kv0) * qw + (q >> 5)], bit) & bit) dup = 1;
+    }
+  }
+  below = wave_incl_sum(below);
+  if (lane == 63) wpart[wave] = below;
+  if (dup) s_dup = 1;
+  __syncthreads();
+  int base = 0;  // edges of this batch-head whose key block is below the range
+#pragma unroll
+  for (int w = 0; w < NW; ++w) base += wpart[w];
+  const bool dups = s_dup != 0;
+  // column counts
+  if (!dups) {
+    for (int c = wave; c < nk; c += NW) {
+      int n = 0;
+      for (int w = lane; w < qw; w += 64) n += __popc(cbits[c * qw + w]);
+      n = wave_incl_sum(n);
+      if (lane == 63) ccount[c] = n;
+    }
+  } else {
+    for (int e = tid; e < edges; e += kCsrNT) {
+      const int kv = sel[e];
+      if (kv >= kv0 && kv < kv0 + nk) atomicAdd(&ccount[kv - kv0], 1);
+    }
   }
   __syncthreads();
-  for (int j = threadIdx.x; j < kb; j += 256) counts[b * kb + j] = cur[j];
+  // exclusive scan of the column counts (nk <= kCsrMaxCols <= kCsrNT), then
+  // counts and offsets out; ccount becomes each column's first slot
+  {
+    const int c = tid < nk ? ccount[tid] : 0;
+    const int incl = wave_incl_sum(c);
+    __syncthreads();  // every count read before wpart and ccount are reused
+    if (lane == 63) wpart[wave] = incl;
+    __syncthreads();
+    int pre = 0;
+    for (int w = 0; w < wave; ++w) pre += wpart[w];
+    if (tid < nk) {
+      const int first = base + pre + incl - c;
+      counts[b * kb + kv0 + tid] = c;
+      offsets[b * kb + kv0 + tid] = first;
+      ccount[tid] = first;
+    }
+  }
   __syncthreads();
-  block_exclusive_scan(cur, kb, tmp);
-  for (int j = threadIdx.x; j < kb; j += 256) offsets[b * kb + j] = cur[j];
-  __syncthreads();
-  int32_t* inv = inverse + b * edges;
-  for (int e = threadIdx.x; e < edges; e += 256) {
-    const int kv = sel[e];
-    if (kv >= 0 && kv < kb) inv[atomicAdd(&cur[kv], 1)] = e / topk;
+  // the segments: a wave per column, ascending query block
+  for (int c = wave; c < nk; c += NW) {
+    int at = ccount[c];
+    if (!dups) {
+      for (int w0 = 0; w0 < qw; w0 += 64) {
+        const int w = w0 + lane;
+        uint32_t word = w < qw ? cbits[c * qw + w] : 0u;
+        const int n = __popc(word);
+        const int incl = wave_incl_sum(n);
+        int pos = at + incl - n;
+        while (word) {
+          const int bit = __builtin_ctz(word);
+          inv[pos++] = w * 32 + bit;
+          word &= word - 1;
+        }
+        at += __shfl(incl, 63, 64);
+      }
+    } else {
+      // ordered scan of the edges: edge e belongs to query block e / topk
+      const int kv = kv0 + c;
+      for (int e0 = 0; e0 < edges; e0 += 64) {
+        const int e = e0 + lane;
+        const bool hit = e < edges && sel[e] == kv;
+        const uint64_t m = __ballot(hit);
+        if (hit) inv[at + __popcll(m & ((1ull << lane) - 1))] = e / topk;
+        at += __popcll(m);
+      }
+    }
   }
 }
 
-__global__ __launch_bounds__(256) void csr_sort_kernel(const int32_t* __restrict__ counts,
-                                                        const int32_t* __restrict__ offsets,
-                                                        int32_t* __restrict__ inverse, int qb,
-                                                        int kb, int topk) {
-  extern __shared__ int ismem[];
-  int* hist = ismem;     // qb
-  int* tmp = hist + qb;  // 256
-  const int64_t b = blockIdx.y;
-  const int kv = blockIdx.x;
-  const int len = counts[b * kb + kv];
-  if (len <= 1) return;  // uniform across the workgroup
-  int32_t* seg = inverse + b * (int64_t)qb * topk + offsets[b * kb + kv];
-  for (int i = threadIdx.x; i < qb; i += 256) hist[i] = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < len; i += 256) atomicAdd(&hist[seg[i]], 1);
-  __syncthreads();
-  block_exclusive_scan(hist, qb, tmp);  // hist[q] -> first slot of q
-  for (int qid = threadIdx.x; qid < qb; qid += 256) {
-    const int start = hist[qid];
-    const int end = qid + 1 < qb ? hist[qid + 1] : len;
-    for (int r = start; r < end; ++r) seg[r] = qid;
-  }
+// Columns per workgroup of csr_cols_kernel: as many as 56 KiB of bits hold, and
+// few enough that the grid has at least about 256 workgroups.
+static int csr_cols_per_wg(int64_t bh, int qb, int kb) {
+  const int qw = (qb + 31) / 32;
+  int per = kCsrBitWords / qw;
+  if (per > kCsrMaxCols) per = kCsrMaxCols;
+  const int64_t splits = (256 + bh - 1) / bh;
+  const int spread = (int)((kb + splits - 1) / splits);
+  if (per > spread) per = spread;
+  return per < 1 ? 1 : per;
 }
 
 // VEC consecutive gate values of element type G as fp32 (16-byte loads), and
@@ -762,7 +826,7 @@ extern "C" int vsa_topk(const float* scores, int32_t* selected, int64_t rows, in
   return topk_radix(scores, selected, rows, kb, topk, (hipStream_t)stream);
 }
 
-constexpr int kMaxCsrBlocks = 16000;  // Kb (or Qb) + 256 ints of LDS stay under 64 KiB
+constexpr int kMaxCsrBlocks = 16000;  // Qb: a column of 500 words, 28 columns per workgroup
 
 extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* offsets,
                              int32_t* inverse, int64_t bh, int32_t qb, int32_t kb, int32_t topk,
@@ -774,13 +838,11 @@ extern "C" int vsa_csr_build(const int32_t* selected, int32_t* counts, int32_t* 
       (int64_t)qb * topk > (1 << 30))
     return VSA_ERR_SHAPE;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(csr_scatter_kernel, dim3((unsigned)bh), dim3(256),
-                     (size_t)(kb + 256) * sizeof(int), s, selected, counts, offsets, inverse,
-                     qb, kb, topk);
-  int rc = vsa_check_launch();
-  if (rc) return rc;
-  hipLaunchKernelGGL(csr_sort_kernel, dim3(kb, (unsigned)bh), dim3(256),
-                     (size_t)(qb + 256) * sizeof(int), s, counts, offsets, inverse, qb, kb, topk);
+  const int per = csr_cols_per_wg(bh, qb, kb);
+  const int qw = (qb + 31) / 32;
+  hipLaunchKernelGGL(csr_cols_kernel, dim3((unsigned)((kb + per - 1) / per), (unsigned)bh),
+                     dim3(kCsrNT), (size_t)per * qw * sizeof(uint32_t), s, selected, counts,
+                     offsets, inverse, qb, kb, topk, per);
   return vsa_check_launch();
 }
 
