@@ -250,10 +250,12 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
     __syncthreads();
     s = s2; ch = ch2; kv = kv2; nvb = nvb2; have = have2;
   };
+  // one exit: a break between the two chunks let the two bodies keep the
+  // accumulators in different registers, with a copy of every accumulator
+  // between them
   while (have) {
     chunk(std::integral_constant<int, 0>{});
-    if (!have) break;
-    chunk(std::integral_constant<int, 1>{});
+    if (have) chunk(std::integral_constant<int, 1>{});
   }
 
   dq_epilogue<T, D, BE, RASTER>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale, orows,
