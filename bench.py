@@ -415,7 +415,7 @@ def main():
     ap.add_argument("--kernels-only", action="store_true", help="skip the CPU baseline and summary")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy a 1 GiB buffer 3 times (calibrates rocprofv3 FETCH/WRITE_SIZE)")
-    ap.add_argument("--workload-steps", type=int, default=5,
+    ap.add_argument("--workload-steps", type=int, default=10,
                     help="timed steps of each other BASELINE configuration (c2, c4, c5) "
                          "reported under 'workloads' of the c3 line; 0 skips them")
     ap.add_argument("--cpu-heads", type=int, default=16,
@@ -577,7 +577,7 @@ def main():
         torch.cuda.empty_cache()
         workloads = {}
         for key in ("c2", "c3tok", "c4", "c5"):
-            r = run_workload(key, args.workload_steps, 2)
+            r = run_workload(key, args.workload_steps, 3)
             workloads[key] = {n: r[n] for n in ("ms_fwd_bwd", "ms_fwd_bwd_median", "ms_fwd",
                                                 "tflops_fwd_bwd",
                                                 "tflops_fwd", "pct_bf16_peak_fwd_bwd",
