@@ -43,17 +43,27 @@ __device__ __forceinline__ void load_rows_b(const T* __restrict__ m, int base, i
 }
 
 // Copy 32 rows of a [rows, D] matrix (rows past the end repeat the last row)
-// into this wave's swizzled LDS tile, for transpose reads.
+// into this wave's swizzled LDS tile, for transpose reads.  Every load is
+// issued before the first LDS store: stored as it arrived, each chunk waited
+// for its own load (one memory round trip per chunk).
 template <typename T, int D>
 __device__ __forceinline__ void stage_rows(T* tile, const T* __restrict__ m, int base, int rows) {
   const int lane = threadIdx.x & 63;
   constexpr int CH = 32 * D / 8;  // 16-byte chunks
+  constexpr int N = CH / 64;      // per lane
+  static_assert(CH % 64 == 0, "whole 16-byte chunks per lane");
+  u32x4 v[N];
 #pragma unroll
-  for (int c = lane; c < CH; c += 64) {
+  for (int i = 0; i < N; ++i) {
+    const int c = lane + 64 * i;
     const int row = c / (D / 8), ch = c % (D / 8);
     const int src = min(base + row, rows - 1);
-    *reinterpret_cast<u32x4*>(tile + swz<D>(row, ch)) =
-        *reinterpret_cast<const u32x4*>(m + (int64_t)src * D + ch * 8);
+    v[i] = *reinterpret_cast<const u32x4*>(m + (int64_t)src * D + ch * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int c = lane + 64 * i;
+    *reinterpret_cast<u32x4*>(tile + swz<D>(c / (D / 8), c % (D / 8))) = v[i];
   }
 }
 
@@ -432,8 +442,12 @@ __global__ __launch_bounds__(256) void coarse_bwd_cols_mfma_kernel(
       for (int e = 0; e < 8; ++e) {
         const int q = t * 32 + 16 * kk + 8 * (e >> 2) + 4 * h + (e & 3);
         const bool ok = q < qb;
-        dsv[e] = ok ? dsb[(int64_t)q * kb + mykey] : 0.f;
-        pv[e] = ok ? pb[(int64_t)q * kb + mykey] : 0.f;
+        // clamped row, loaded unconditionally (a load under the condition
+        // became a branch and a wait per value), zeroed after
+        const int64_t at = (int64_t)min(q, qb - 1) * kb + mykey;
+        const float dl = dsb[at], pl = pb[at];
+        dsv[e] = ok ? dl : 0.f;
+        pv[e] = ok ? pl : 0.f;
       }
       const V8 bs = pack8<T>(dsv);
       const V8 bp = pack8<T>(pv);
