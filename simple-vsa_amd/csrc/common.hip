@@ -3,6 +3,7 @@
 // routing, backward preprocessing (delta + combine gradients) and the coarse
 // branch backward.  The MFMA fine kernels live in fine_fwd.hip / fine_bwd.hip.
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 
 #include "coarse.h"
@@ -380,6 +381,44 @@ __device__ __forceinline__ void load_gate(const G* __restrict__ p, float* out) {
   }
 }
 
+// The same VEC values kept as the raw 16-byte chunks, for a caller that issues
+// the loads of several rows before converting any of them (a conversion right
+// after each load would make every row wait for its own load).
+template <typename G, int VEC>
+struct GateRaw {
+  static constexpr int N = VEC * (int)sizeof(G) / 16;
+  u32x4 c[N];
+  __device__ __forceinline__ void load(const G* __restrict__ p) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) c[i] = *reinterpret_cast<const u32x4*>(p + i * (16 / sizeof(G)));
+  }
+  __device__ __forceinline__ float at(int e) const {
+    return Elem<G>::to_f(reinterpret_cast<const G*>(c)[e]);
+  }
+};
+
+// One gate value's bits, zero-extended to 32 (a 16-bit value loaded into half
+// of a register shared with other data would be merged, and waited for, at
+// once), and its value as fp32.
+template <typename G>
+__device__ __forceinline__ uint32_t load_bits(const G* p) {
+  if constexpr (sizeof(G) == 2)
+    return *reinterpret_cast<const uint16_t*>(p);
+  else
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+template <typename G>
+__device__ __forceinline__ float bits_to_f(uint32_t b) {
+  G g;
+  if constexpr (sizeof(G) == 2) {
+    const uint16_t h = (uint16_t)b;
+    __builtin_memcpy(&g, &h, 2);
+  } else {
+    __builtin_memcpy(&g, &b, 4);
+  }
+  return Elem<G>::to_f(g);
+}
+
 template <typename G, int VEC>
 __device__ __forceinline__ void store_gate(G* __restrict__ p, const float* v) {
   constexpr int PER = 16 / (int)sizeof(G);
@@ -407,79 +446,82 @@ __device__ __forceinline__ void store_gate(G* __restrict__ p, const float* v) {
 // at the padding slots) for the fine backward kernels.  Every value is then
 // what the tiled pass computes after tile() of dout and of the gate.
 // ---------------------------------------------------------------------------
-template <typename T, typename G, bool RASTER = false>
-__global__ __launch_bounds__(256) void bwd_prep_kernel(
+// GM is the gate mode, fixed at compile time so that each row's loads and
+// arithmetic are straight-line code: -1 no coarse output (delta only), 0
+// coarse output without a gate, 1 full gate [.., S, D], 2 per-token gate
+// [.., S], 3 full gate in the token-major layout [B, S, H, D].
+template <typename T, typename G, int GM, bool RASTER>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RASTER ? 3 : 4))) void bwd_prep_kernel(
     const T* __restrict__ fine, const T* __restrict__ dout, const T* __restrict__ outc,
-    const G* __restrict__ gate, int gate_mode, int gate_heads, float* __restrict__ delta,
+    const G* __restrict__ gate, int gate_heads, float* __restrict__ delta,
     T* __restrict__ d_outc, G* __restrict__ d_gate, int qb, int D, int be,
-    const int32_t* __restrict__ rows = nullptr, int64_t s_out = 0, int heads = 0,
-    T* __restrict__ dout_t = nullptr) {
+    const int32_t* __restrict__ rows, int64_t s_out, int heads, T* __restrict__ dout_t) {
   constexpr int VEC = 16 / sizeof(T);
-  __shared__ float part[256 * VEC];
+  constexpr bool OC = GM >= 0;                  // coarse output present
+  constexpr bool FULL = GM == 1 || GM == 3;     // a gate value per element
+  __shared__ float part[OC ? 256 * VEC : 1];
   const int64_t blk = blockIdx.x + (int64_t)blockIdx.y * qb;  // bh*qb + n
   const int tpr = D / VEC, rpi = 256 / tpr;
   const int col = threadIdx.x % tpr, row0 = threadIdx.x / tpr;
   const int c0 = col * VEC;
   float oc[VEC], dacc[VEC];
+  if constexpr (OC) {
+    // one 16-byte load (element-wise loads would each wait for the previous)
+    const u32x4 ocr = *reinterpret_cast<const u32x4*>(outc + blk * D + c0);
+    const T* ocv = reinterpret_cast<const T*>(&ocr);
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    oc[e] = outc ? Elem<T>::to_f(outc[blk * D + c0 + e]) : 0.f;
-    dacc[e] = 0.f;
+    for (int e = 0; e < VEC; ++e) {
+      oc[e] = Elem<T>::to_f(ocv[e]);
+      dacc[e] = 0.f;
+    }
   }
   // token-major gate [B, Sq, H, D]: element (bh = b*H + h, s, d) at ((b*Sq + s)*H + h)*D + d
   const int64_t bh = blockIdx.y;
   const int64_t sq = (int64_t)qb * be;
-  const int64_t gbase = gate_mode == 3
-                            ? ((bh / gate_heads) * sq * gate_heads + bh % gate_heads) * D + c0
-                            : 0;
+  const int64_t gbase =
+      GM == 3 ? ((bh / gate_heads) * sq * gate_heads + bh % gate_heads) * D + c0 : 0;
   // UR rows per pass: their loads are issued together and their row
   // reductions run as UR independent chains (one row per pass left a single
   // load and a serial shuffle chain per iteration)
   constexpr int UR = 4;
   for (int t0 = row0; t0 < be; t0 += UR * rpi) {
     u32x4 ro[UR], rd[UR];
-    float gv[UR][VEC];
-    int64_t rtok[UR];  // RASTER: raster token of row t (-1: padding slot)
+    GateRaw<G, VEC> graw[UR];  // full gate chunks as loaded
+    uint32_t gtok[UR];         // per-token gate value's bits as loaded
+    // RASTER: whether slot t holds a token, and the raster token its dout and
+    // gate rows are read from (token 0 of the head for a padding slot, whose
+    // values are then replaced by zeros)
+    bool real[UR];
+    int64_t rtok[UR];
+    if constexpr (RASTER) {
+      int r[UR];
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        const int t = t0 + u * rpi;
+        if (t >= be) break;
+        r[u] = rows[(int64_t)blockIdx.x * be + t];
+      }
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        if (t0 + u * rpi >= be) break;
+        real[u] = r[u] >= 0 && r[u] < s_out;
+        rtok[u] = raster_row(bh, real[u] ? r[u] : 0, s_out, heads);
+      }
+    }
+    // every row's loads are issued before any of them is used (a value used
+    // right after its load would make each row wait for its own)
 #pragma unroll
     for (int u = 0; u < UR; ++u) {
       const int t = t0 + u * rpi;
       if (t >= be) break;
       const int64_t tok = blk * be + t;
-      const int64_t off = tok * D + c0;
-      ro[u] = ld_stream(reinterpret_cast<const u32x4*>(fine + off));
-      if constexpr (RASTER) {
-        const int r = rows[(int64_t)blockIdx.x * be + t];
-        rtok[u] = (r >= 0 && r < s_out) ? raster_row(bh, r, s_out, heads) : -1;
-        const bool real = rtok[u] >= 0;
-        rd[u] = real ? ld_stream(reinterpret_cast<const u32x4*>(dout + rtok[u] * D + c0))
-                     : u32x4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(dout_t + off) = rd[u];
-        if (gate_mode == 1) {
-          if (real) {
-            load_gate<G, VEC>(gate + rtok[u] * D + c0, gv[u]);
-          } else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) gv[u][e] = 0.f;
-          }
-        } else {
-          const float gs = gate_mode == 2 ? (real ? Elem<G>::to_f(gate[rtok[u]]) : 0.f) : 1.f;
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) gv[u][e] = gs;
-        }
-        continue;
-      }
-      rd[u] = ld_stream(reinterpret_cast<const u32x4*>(dout + off));
-      if (gate_mode == 1 || gate_mode == 3) {
-        // offset of this token's gate (and d_gate) chunk
-        const int64_t goff = gate_mode == 3
-                                 ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
-                                 : off;
-        load_gate<G, VEC>(gate + goff, gv[u]);
-      } else {
-        const float gs = gate_mode == 2 ? Elem<G>::to_f(gate[tok]) : 1.f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) gv[u][e] = gs;
-      }
+      ro[u] = ld_stream(reinterpret_cast<const u32x4*>(fine + tok * D + c0));
+      const int64_t src = RASTER ? rtok[u] : tok;   // dout / gate token
+      rd[u] = ld_stream(reinterpret_cast<const u32x4*>(dout + src * D + c0));
+      if constexpr (GM == 1) graw[u].load(gate + src * D + c0);
+      if constexpr (GM == 3)
+        graw[u].load(gate + gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D);
+      if constexpr (GM == 2) gtok[u] = load_bits(gate + src);
     }
     float dl[UR], dg[UR];
 #pragma unroll
@@ -488,6 +530,11 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
     for (int u = 0; u < UR; ++u) {
       const int t = t0 + u * rpi;
       if (t >= be) break;
+      const bool pad = RASTER && !real[u];   // a padding slot: dout and gate read as zero
+      if constexpr (RASTER) {
+        if (pad) rd[u] = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(dout_t + (blk * be + t) * D + c0) = rd[u];
+      }
       const T* o = reinterpret_cast<const T*>(&ro[u]);
       const T* g = reinterpret_cast<const T*>(&rd[u]);
       float dgv[VEC];  // this chunk of d_gate (full gate), stored with 16-byte writes
@@ -495,19 +542,22 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       for (int e = 0; e < VEC; ++e) {
         const float dov = Elem<T>::to_f(g[e]);
         dl[u] = fmaf(Elem<T>::to_f(o[e]), dov, dl[u]);
-        dgv[e] = dov * oc[e];
-        if (outc) {
-          dacc[e] += gate_mode == 0 ? dov : round_t<T>(dov * gv[u][e]);
-          if (gate_mode == 2) dg[u] = fmaf(dov, oc[e], dg[u]);
+        if constexpr (GM == 0) dacc[e] += dov;
+        if constexpr (FULL) {
+          dgv[e] = dov * oc[e];
+          dacc[e] += round_t<T>(dov * (pad ? 0.f : graw[u].at(e)));
+        }
+        if constexpr (GM == 2) {
+          dacc[e] += round_t<T>(dov * (pad ? 0.f : bits_to_f<G>(gtok[u])));
+          dg[u] = fmaf(dov, oc[e], dg[u]);
         }
       }
-      if (outc && (gate_mode == 1 || gate_mode == 3)) {
+      if constexpr (FULL) {
         if constexpr (RASTER) {
-          if (rtok[u] >= 0) store_gate<G, VEC>(d_gate + rtok[u] * D + c0, dgv);
+          if (real[u]) store_gate<G, VEC>(d_gate + rtok[u] * D + c0, dgv);
         } else {
-          const int64_t goff = gate_mode == 3
-                                   ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
-                                   : (blk * be + t) * D + c0;
+          const int64_t goff = GM == 3 ? gbase + ((int64_t)blockIdx.x * be + t) * gate_heads * D
+                                       : (blk * be + t) * D + c0;
           store_gate<G, VEC>(d_gate + goff, dgv);
         }
       }
@@ -517,7 +567,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
 #pragma unroll
       for (int u = 0; u < UR; ++u) {
         dl[u] += __shfl_xor(dl[u], o2, 64);
-        dg[u] += __shfl_xor(dg[u], o2, 64);
+        if constexpr (GM == 2) dg[u] += __shfl_xor(dg[u], o2, 64);
       }
     }
     if (col == 0) {
@@ -527,15 +577,14 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
         if (t >= be) break;
         const int64_t tok = blk * be + t;
         delta[tok] = dl[u];
-        if constexpr (RASTER) {
-          if (outc && gate_mode == 2 && rtok[u] >= 0) d_gate[rtok[u]] = Elem<G>::from_f(dg[u]);
-        } else {
-          if (outc && gate_mode == 2) d_gate[tok] = Elem<G>::from_f(dg[u]);
+        if constexpr (GM == 2) {
+          if (!RASTER) d_gate[tok] = Elem<G>::from_f(dg[u]);
+          else if (real[u]) d_gate[rtok[u]] = Elem<G>::from_f(dg[u]);
         }
       }
     }
   }
-  if (outc) {
+  if constexpr (OC) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) part[row0 * D + c0 + e] = dacc[e];
     __syncthreads();
@@ -544,6 +593,30 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(
       for (int r = 0; r < rpi; ++r) s += part[r * D + d];
       d_outc[blk * D + d] = Elem<T>::from_f(s);
     }
+  }
+}
+
+// Launches the bwd_prep_kernel instance of gate mode gm (-1..3; 3 only in the
+// tiled layout, -1 and 0 only with G == T).
+template <typename T, typename G, bool RASTER>
+static void launch_bwd_prep(int gm, dim3 grid, hipStream_t s, const T* fine, const T* dout,
+                            const T* outc, const G* gate, int gate_heads, float* delta,
+                            T* d_outc, G* d_gate, int qb, int D, int be, const int32_t* rows,
+                            int64_t s_out, int heads, T* dout_t) {
+  auto go = [&](auto mode) {
+    constexpr int GM = decltype(mode)::value;
+    hipLaunchKernelGGL((bwd_prep_kernel<T, G, GM, RASTER>), grid, dim3(256), 0, s, fine, dout,
+                       outc, gate, gate_heads, delta, d_outc, d_gate, qb, D, be, rows, s_out,
+                       heads, dout_t);
+  };
+  if constexpr (std::is_same<G, T>::value) {
+    if (gm == -1) go(std::integral_constant<int, -1>{});
+    if (gm == 0) go(std::integral_constant<int, 0>{});
+  }
+  if (gm == 1) go(std::integral_constant<int, 1>{});
+  if (gm == 2) go(std::integral_constant<int, 2>{});
+  if constexpr (!RASTER) {
+    if (gm == 3) go(std::integral_constant<int, 3>{});
   }
 }
 
@@ -864,16 +937,18 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
     return VSA_ERR_SHAPE;
   const int qb = (int)(sq / be);
   hipStream_t s = (hipStream_t)stream;
+  const int gm = out_c ? gate_mode : -1;
+  const dim3 grid(qb, (unsigned)bh);
   VSA_DISPATCH_ALL(dtype, T, {
-    if (gate_f32)
-      hipLaunchKernelGGL((bwd_prep_kernel<T, float>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
-                         (const T*)fine_out, (const T*)dout, (const T*)out_c,
-                         (const float*)gate, gate_mode, gate_heads, delta, (T*)d_out_c,
-                         (float*)d_gate, qb, D, be);
+    if (gate_f32 && gm > 0)
+      (launch_bwd_prep<T, float, false>)(gm, grid, s, (const T*)fine_out, (const T*)dout,
+                                       (const T*)out_c, (const float*)gate, gate_heads, delta,
+                                       (T*)d_out_c, (float*)d_gate, qb, D, be, nullptr, 0, 0,
+                                       nullptr);
     else
-      hipLaunchKernelGGL((bwd_prep_kernel<T, T>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
-                         (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate,
-                         gate_mode, gate_heads, delta, (T*)d_out_c, (T*)d_gate, qb, D, be);
+      (launch_bwd_prep<T, T, false>)(gm, grid, s, (const T*)fine_out, (const T*)dout,
+                                   (const T*)out_c, (const T*)gate, gate_heads, delta,
+                                   (T*)d_out_c, (T*)d_gate, qb, D, be, nullptr, 0, 0, nullptr);
   });
   return vsa_check_launch();
 }
@@ -897,11 +972,12 @@ extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const 
     return VSA_ERR_SHAPE;
   const int qb = (int)(sq / be);
   hipStream_t s = (hipStream_t)stream;
+  const int gm = out_c ? gate_mode : -1;
   VSA_DISPATCH_ALL(dtype, T, {
-    hipLaunchKernelGGL((bwd_prep_kernel<T, T, true>), dim3(qb, (unsigned)bh), dim3(256), 0, s,
-                       (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate,
-                       gate_mode, 1, delta, (T*)d_out_c, (T*)d_gate, qb, D, be, slot_rows, s_out,
-                       heads, (T*)dout_t);
+    (launch_bwd_prep<T, T, true>)(gm, dim3(qb, (unsigned)bh), s, (const T*)fine_out,
+                                (const T*)dout, (const T*)out_c, (const T*)gate, 1, delta,
+                                (T*)d_out_c, (T*)d_gate, qb, D, be, slot_rows, s_out, heads,
+                                (T*)dout_t);
   });
   return vsa_check_launch();
 }
