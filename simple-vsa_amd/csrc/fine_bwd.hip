@@ -163,11 +163,15 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   // tr_a8 compute: the swizzle repeats every 16 rows, so rows 32*smt + r sit
   // at row_off[ks] + 32*smt*D*2 and the transposed pieces of keys 16*kk + ..
   // at tr_off[mt][hi] + 16*kk*D*2; left to the compiler, that arithmetic was
-  // redone for every chunk).
+  // redone for every chunk).  At head dim 256 the 32 offsets, held across the
+  // chunk loop next to the 512 registers of fragments and accumulators, made
+  // the kernel spill inside the loop (dQ 8.1 -> 10.5 ms at 20 heads x 40 960
+  // tokens): there the offsets are formed per read and the loop keeps one body.
+  constexpr bool LANE_OFFSETS = D <= 128;
   uint32_t row_off[D / 16], tr_off[D / 32][2];
+  if constexpr (LANE_OFFSETS) {
 #pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks) row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * sizeof(T)));
-  {
+    for (int ks = 0; ks < D / 16; ++ks) row_off[ks] = opaque((uint32_t)(swz<D>(r, 2 * ks + h) * sizeof(T)));
     const int grp = lane >> 4, jl = lane & 15, qq = grp & 1, hh = grp >> 1;
 #pragma unroll
     for (int mt = 0; mt < D / 32; ++mt)
@@ -178,19 +182,26 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   }
   const char* smem_c = reinterpret_cast<const char*>(smem);
   auto t_row = [&](int stg, int tilesel, int ks, int smt) {  // K (tilesel 0) or V rows 32*smt + r
-    return as_vec8<T>(*reinterpret_cast<const u32x4*>(
-        smem_c + (stg * C::STAGE + tilesel * C::TILE + smt * 32 * D) * (int)sizeof(T) + row_off[ks]));
+    if constexpr (!LANE_OFFSETS)
+      return row_a8<T, D>(smem + stg * C::STAGE + tilesel * C::TILE, smt * 32 + r, ks, h);
+    else
+      return as_vec8<T>(*reinterpret_cast<const u32x4*>(
+          smem_c + (stg * C::STAGE + tilesel * C::TILE + smt * 32 * D) * (int)sizeof(T) + row_off[ks]));
   };
   auto k_tr = [&](int stg, int mt, int kk) {  // K^T pieces, keys 16kk ..
-    const char* base = smem_c + (stg * C::STAGE + kk * 16 * D) * (int)sizeof(T);
-    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][0]));
-    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][1]));
-    u32x4 rr;
-    rr[0] = __builtin_bit_cast(u32x2, lo)[0];
-    rr[1] = __builtin_bit_cast(u32x2, lo)[1];
-    rr[2] = __builtin_bit_cast(u32x2, hi)[0];
-    rr[3] = __builtin_bit_cast(u32x2, hi)[1];
-    return as_vec8<T>(rr);
+    if constexpr (!LANE_OFFSETS) {
+      return tr_a8<T, D>(smem + stg * C::STAGE, mt * 32, 16 * kk, 16 * kk + 8);
+    } else {
+      const char* base = smem_c + (stg * C::STAGE + kk * 16 * D) * (int)sizeof(T);
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][0]));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + tr_off[mt][1]));
+      u32x4 rr;
+      rr[0] = __builtin_bit_cast(u32x2, lo)[0];
+      rr[1] = __builtin_bit_cast(u32x2, lo)[1];
+      rr[2] = __builtin_bit_cast(u32x2, hi)[0];
+      rr[3] = __builtin_bit_cast(u32x2, hi)[1];
+      return as_vec8<T>(rr);
+    }
   };
 
   RouteRegs<BE, C::KC> route{sel, kv_vbs, topk, kb};
@@ -200,10 +211,11 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   if (have) dma(kv, ch, 0);
   dma_wait();
   __syncthreads();
-  // one chunk on stage stg (the loop below is unrolled by the two stages, so
-  // that every LDS address is a lane offset plus an immediate)
+  // one chunk on stage stage_c (with lane offsets the loop below is unrolled
+  // by the two stages, so that every LDS address is a lane offset plus an
+  // immediate)
   auto chunk = [&](auto stage_c) {
-    constexpr int stage = decltype(stage_c)::value;
+    const int stage = stage_c;
     const int nv = min(nvb - ch * C::KC, C::KC);
     int s2 = s, ch2 = ch + 1, kv2 = kv, nvb2 = nvb;
     const bool have2 = route.next(s2, ch2, kv2, nvb2);
@@ -253,9 +265,13 @@ sparse_dq_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __re
   // one exit: a break between the two chunks let the two bodies keep the
   // accumulators in different registers, with a copy of every accumulator
   // between them
-  while (have) {
-    chunk(std::integral_constant<int, 0>{});
-    if (have) chunk(std::integral_constant<int, 1>{});
+  if constexpr (LANE_OFFSETS) {
+    while (have) {
+      chunk(std::integral_constant<int, 0>{});
+      if (have) chunk(std::integral_constant<int, 1>{});
+    }
+  } else {
+    for (int stage = 0; have; stage ^= 1) chunk(stage);
   }
 
   dq_epilogue<T, D, BE, RASTER>(dqacc, b, myq, qblk, h, sq, qb, dq, dqc, q_vbs, scale, orows,
