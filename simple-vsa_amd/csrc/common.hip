@@ -597,9 +597,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RASTER ? 3 
 }
 
 // Launches the bwd_prep_kernel instance of gate mode gm (-1..3; 3 only in the
-// tiled layout, -1 and 0 only with G == T).
+// tiled layout, -1 and 0 only with G == T); false when there is none.
 template <typename T, typename G, bool RASTER>
-static void launch_bwd_prep(int gm, dim3 grid, hipStream_t s, const T* fine, const T* dout,
+static bool launch_bwd_prep(int gm, dim3 grid, hipStream_t s, const T* fine, const T* dout,
                             const T* outc, const G* gate, int gate_heads, float* delta,
                             T* d_outc, G* d_gate, int qb, int D, int be, const int32_t* rows,
                             int64_t s_out, int heads, T* dout_t) {
@@ -610,14 +610,15 @@ static void launch_bwd_prep(int gm, dim3 grid, hipStream_t s, const T* fine, con
                        heads, dout_t);
   };
   if constexpr (std::is_same<G, T>::value) {
-    if (gm == -1) go(std::integral_constant<int, -1>{});
-    if (gm == 0) go(std::integral_constant<int, 0>{});
+    if (gm == -1) return go(std::integral_constant<int, -1>{}), true;
+    if (gm == 0) return go(std::integral_constant<int, 0>{}), true;
   }
-  if (gm == 1) go(std::integral_constant<int, 1>{});
-  if (gm == 2) go(std::integral_constant<int, 2>{});
+  if (gm == 1) return go(std::integral_constant<int, 1>{}), true;
+  if (gm == 2) return go(std::integral_constant<int, 2>{}), true;
   if constexpr (!RASTER) {
-    if (gm == 3) go(std::integral_constant<int, 3>{});
+    if (gm == 3) return go(std::integral_constant<int, 3>{}), true;
   }
+  return false;
 }
 
 // ---------------------------------------------------------------------------
@@ -939,17 +940,18 @@ extern "C" int vsa_bwd_prep(const void* fine_out, const void* dout, const void* 
   hipStream_t s = (hipStream_t)stream;
   const int gm = out_c ? gate_mode : -1;
   const dim3 grid(qb, (unsigned)bh);
+  bool launched = false;
   VSA_DISPATCH_ALL(dtype, T, {
     if (gate_f32 && gm > 0)
-      (launch_bwd_prep<T, float, false>)(gm, grid, s, (const T*)fine_out, (const T*)dout,
-                                       (const T*)out_c, (const float*)gate, gate_heads, delta,
-                                       (T*)d_out_c, (float*)d_gate, qb, D, be, nullptr, 0, 0,
-                                       nullptr);
+      launched = (launch_bwd_prep<T, float, false>)(
+          gm, grid, s, (const T*)fine_out, (const T*)dout, (const T*)out_c, (const float*)gate,
+          gate_heads, delta, (T*)d_out_c, (float*)d_gate, qb, D, be, nullptr, 0, 0, nullptr);
     else
-      (launch_bwd_prep<T, T, false>)(gm, grid, s, (const T*)fine_out, (const T*)dout,
-                                   (const T*)out_c, (const T*)gate, gate_heads, delta,
-                                   (T*)d_out_c, (T*)d_gate, qb, D, be, nullptr, 0, 0, nullptr);
+      launched = (launch_bwd_prep<T, T, false>)(
+          gm, grid, s, (const T*)fine_out, (const T*)dout, (const T*)out_c, (const T*)gate,
+          gate_heads, delta, (T*)d_out_c, (T*)d_gate, qb, D, be, nullptr, 0, 0, nullptr);
   });
+  if (!launched) return VSA_ERR_SHAPE;
   return vsa_check_launch();
 }
 
@@ -973,12 +975,14 @@ extern "C" int vsa_bwd_prep_tiled(const void* fine_out, const void* dout, const 
   const int qb = (int)(sq / be);
   hipStream_t s = (hipStream_t)stream;
   const int gm = out_c ? gate_mode : -1;
+  bool launched = false;
   VSA_DISPATCH_ALL(dtype, T, {
-    (launch_bwd_prep<T, T, true>)(gm, dim3(qb, (unsigned)bh), s, (const T*)fine_out,
-                                (const T*)dout, (const T*)out_c, (const T*)gate, 1, delta,
-                                (T*)d_out_c, (T*)d_gate, qb, D, be, slot_rows, s_out, heads,
-                                (T*)dout_t);
+    launched = (launch_bwd_prep<T, T, true>)(
+        gm, dim3(qb, (unsigned)bh), s, (const T*)fine_out, (const T*)dout, (const T*)out_c,
+        (const T*)gate, 1, delta, (T*)d_out_c, (T*)d_gate, qb, D, be, slot_rows, s_out, heads,
+        (T*)dout_t);
   });
+  if (!launched) return VSA_ERR_SHAPE;
   return vsa_check_launch();
 }
 
